@@ -1,0 +1,282 @@
+"""Benchmark of the paged-attention hot path on one MI355X.
+
+A step is one pass of the path over one batch: append the new tokens' K/V
+into their pages, then paged attention (decode: one query per sequence;
+prefill: ragged causal chunks).  The plan is built once per batch (the engine
+builds it once per forward and reuses it across layers).
+
+Default workload: TinyLlama-1.1B paged decode at scale (32q/4kv heads, D=64,
+page 16, B=256, kv_len U[256,2048], bf16).  `value` is whole-step
+throughput in algorithmic HBM GB/s; `roofline` is the decode attention
+launch (algorithmic bytes / average launch time from HIP events);
+`cpu_baseline` is the fp32 CPU oracle on a bounded sample of the same batch.
+Pools are rotated across replicas totalling > 1 GB so the 256 MB Infinity
+Cache cannot hold the KV between steps.
+
+Prints ONE JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "llm-inference-runtime_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+WS_BYTES = 128 << 20
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _replicas(bytes_per_instance: int, min_total: int = 1 << 30, cap: int = 8) -> int:
+    r = 1
+    while r * bytes_per_instance < min_total and r < cap:
+        r += 1
+    return r
+
+
+def bench_decode(w, args, dev, dtype, label, cpu_sample: int = 0):
+    import numpy as np
+    import torch
+
+    import pagedattn
+    from pagedattn import workloads as W
+
+    kv_elem = 1 if w.fp8 else 2
+    alg_attn = W.decode_bytes(w, kv_elem)
+    alg_step = W.decode_bytes(w, kv_elem, with_append=True)
+    pool_bytes = w.num_pages * 2 * w.hkv * 16 * w.d * kv_elem
+    reps = _replicas(pool_bytes)
+    log(f"{label}: B={w.meta.batch_size} pages={w.num_pages} kv={alg_attn / 1e9:.3f} GB "
+        f"replicas={reps}")
+    inst = []
+    for r in range(reps):
+        t = W.materialize(w, dev, dtype, seed=w.seed * 100 + r)
+        if w.fp8:
+            t.pool, t.scales = pagedattn.quantize_pages_e4m3(t.pool)
+        inst.append(t)
+    torch.cuda.synchronize()
+    ws = torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
+    dw = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    t0 = inst[0]
+    tp = time.perf_counter()
+    dw.plan(t0.kv_indptr, t0.kv_indices, t0.kv_last_page_len, w.hq, w.hkv, w.d, 16,
+            q_data_type=dtype, split_pages=w.split_pages)
+    torch.cuda.synchronize()
+    plan_ms = (time.perf_counter() - tp) * 1e3
+    outs = [torch.empty((w.meta.batch_size, w.hq, w.d), dtype=dtype, device=dev)
+            for _ in range(reps)]
+
+    def step(i, ev=None):
+        t = inst[i % reps]
+        pagedattn.append_paged_kv_cache(t.k_new, t.v_new, t.batch_indices, t.positions, t.pool,
+                                        t.kv_indices, t.kv_indptr, t.kv_last_page_len,
+                                        kv_layout="HND", kv_scales=t.scales)
+        if ev is not None:
+            ev[0].record()
+        dw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps])
+        if ev is not None:
+            ev[1].record()
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    attn_ms = [a.elapsed_time(b) for a, b in evs]
+    attn_avg = sum(attn_ms) / len(attn_ms)
+    res = {
+        "workload": label,
+        "ms_per_step": total_ms / args.steps,
+        "step_GBps": alg_step / (total_ms / args.steps * 1e-3) / 1e9,
+        "attn_ms_avg": attn_avg,
+        "attn_ms_median": float(np.median(attn_ms)),
+        "attn_GBps": alg_attn / (attn_avg * 1e-3) / 1e9,
+        "alg_bytes_attn": alg_attn,
+        "alg_bytes_step": alg_step,
+        "plan_ms_host": plan_ms,
+        "replicas": reps,
+        "batch": w.meta.batch_size,
+        "kv_tokens": int(w.meta.seq_lens.sum()),
+        "split_pages": w.split_pages,
+    }
+    res["attn_frac"] = res["attn_GBps"] / HBM_PEAK_GBS
+    if cpu_sample:
+        res["cpu"] = cpu_decode_baseline(w, inst[0], cpu_sample, kv_elem)
+    del inst, outs
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_decode_baseline(w, t, n_seq: int, kv_elem: int):
+    """fp32 oracle decode over the first n_seq sequences, timed on the host."""
+    import numpy as np
+    import torch
+
+    import oracle as O
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rows = list(range(min(n_seq, w.meta.batch_size)))
+    m = w.meta
+    # compact pool of the sampled sequences, copied to host once (untimed)
+    parts = [m.kv_indices[m.kv_indptr[b]:m.kv_indptr[b + 1]] for b in rows]
+    pages = np.concatenate(parts)
+    indptr = np.concatenate([[0], np.cumsum([len(p) for p in parts])]).astype(np.int32)
+    idx = torch.from_numpy(pages.astype(np.int64)).to(t.pool.device)
+    sub = t.pool.index_select(0, idx).cpu()
+    scales = None if t.scales is None else t.scales.index_select(0, idx).cpu()
+    q = t.q[rows].float().cpu()
+    ind = np.arange(len(pages), dtype=np.int32)
+    last = m.kv_last_page_len[rows]
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.decode(q, sub, indptr, ind, last, scales=scales)
+        times.append(time.perf_counter() - t0)
+    sec = float(np.median(times))
+    kv_bytes = int(m.seq_lens[rows].astype(np.int64).sum()) * w.hkv * w.d * 2 * kv_elem
+    byts = kv_bytes + len(rows) * w.hq * w.d * 4
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
+                         "unknown")
+    except OSError:
+        model = "unknown"
+    return {
+        "value": byts / sec / 1e9,
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"{len(rows)} of {w.meta.batch_size} sequences of {w.name} "
+                   f"({int(m.seq_lens[rows].sum())} kv tokens), fp32 torch oracle, "
+                   f"median of 3 = {sec:.3f} s on {model}"),
+    }
+
+
+def copy_calibration(dev, nbytes: int = 1 << 30, reps: int = 3) -> dict:
+    """A plain copy of known size: the reference point for HBM byte counters."""
+    import torch
+
+    import pagedattn
+
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        pagedattn.copy_bytes(dst, src)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    pagedattn.copy_bytes(dst, src)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b)
+    return {"bytes_read": nbytes, "bytes_written": nbytes, "ms": ms,
+            "GBps": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the other workloads (long-context decode, ...)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported",
+              file=sys.stderr)
+        return 2
+    import torch
+
+    from pagedattn import workloads as W
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    dtype = torch.bfloat16
+
+    main_w = W.tinyllama_decode(seed=args.seed)
+    r = bench_decode(main_w, args, dev, dtype, "tinyllama_decode",
+                     cpu_sample=0 if args.no_cpu else 64)
+    log(f"tinyllama_decode: step {r['ms_per_step']:.4f} ms, attention {r['attn_ms_avg']:.4f} ms "
+        f"= {r['attn_GBps']:.0f} GB/s ({100 * r['attn_frac']:.1f}% of 8 TB/s)")
+    extra = {}
+    if not args.no_extra:
+        lw = W.llama3_8b_long_decode(seed=args.seed)
+        lr = bench_decode(lw, argparse.Namespace(steps=max(5, args.steps // 3),
+                                                 warmup=2), dev, dtype,
+                          "llama3_8b_long_decode")
+        log(f"llama3_8b_long_decode: attention {lr['attn_ms_avg']:.3f} ms = "
+            f"{lr['attn_GBps']:.0f} GB/s ({100 * lr['attn_frac']:.1f}%)")
+        extra["llama3_8b_long_decode"] = {k: lr[k] for k in (
+            "ms_per_step", "attn_ms_avg", "attn_GBps", "attn_frac", "alg_bytes_attn",
+            "split_pages", "batch", "kv_tokens")}
+    cal = copy_calibration(dev)
+    log(f"copy calibration: {cal['GBps']:.0f} GB/s (read+write)")
+
+    line = {
+        "metric": "paged decode attn HBM GB/s (% of 8 TB/s); prefill attn TFLOP/s (% MFMA peak)",
+        "value": round(r["step_GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) pool/q/k/v, random block tables)",
+        "config": {
+            "workload": "tinyllama_decode: TinyLlama-1.1B paged decode at scale, 32q/4kv heads, "
+                        "head_dim 64, page 16, batch 256, kv_len U[256,2048], fused append",
+            "batch": r["batch"],
+            "kv_tokens": r["kv_tokens"],
+            "page_size": 16,
+            "parallelism": "single GPU",
+            "seed": args.seed,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "decode attention launch (pagedattn decode_kernel<64,bf16>)",
+            "achieved": round(r["attn_GBps"], 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(r["attn_frac"], 4),
+            "traffic": None,
+            "alg_bytes_per_launch": r["alg_bytes_attn"],
+            "avg_launch_ms": round(r["attn_ms_avg"], 5),
+        },
+        "cpu_baseline": r.get("cpu"),
+        "extra": extra,
+        "copy_calibration": cal,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,213 @@
+/*
+ * pagedattn.h - C ABI of the MI355X (gfx950) paged-attention module.
+ *
+ * One shared library (libpagedattn.so) exports these entry points.  They
+ * replace the FlashInfer calls that the serving engine's patched
+ * LlamaAttention.forward makes (src/models/llama.py:39-249): batch planning,
+ * RoPE, page append and paged prefill / decode attention.
+ *
+ * Conventions for every entry point:
+ *   - Device pointers are plain `void*` / typed pointers to device memory
+ *     (HBM of the current HIP device); "_host" pointers are host memory.
+ *   - Strides are in elements, not bytes; the innermost (head_dim) axis must
+ *     be contiguous.
+ *   - `stream` is a hipStream_t passed as `void*` (NULL = default stream).
+ *     Every kernel is launched on it; nothing synchronises the device.
+ *   - The return value is 0 on success or one of the PAGEDATTN_ERR_* codes.
+ *     A human-readable message for the last failure on the calling thread is
+ *     available from pagedattn_last_error().  Invalid arguments are rejected
+ *     on the host before any launch; device-side index checks skip (never
+ *     fault on) out-of-range metadata and count it in `error_flag` where the
+ *     call takes one.
+ *   - kv_indices arguments come with num_indices, the number of valid
+ *     entries; kernels never read past it (a page slot whose index would lie
+ *     beyond it is treated as absent).
+ *   - The library never allocates device memory.  Work lists and split-KV
+ *     partials live in the caller's workspace buffer (128 MiB in the engine,
+ *     src/models/llama.py:49-53).
+ *
+ * KV pool layout ("HND", src/engine/memory/allocator.py:25-36): one layer is
+ * a contiguous [num_pages, 2, num_kv_heads, page_size, head_dim] array; K of
+ * (page p, head h) is the page_size x head_dim block at element offset
+ * ((p*2+0)*num_kv_heads+h)*page_size*head_dim, V at ((p*2+1)*...).
+ * fp8 pools store OCP e4m3fn bytes in the same layout plus fp32 scales
+ * [num_pages, 2, num_kv_heads]; the stored value is round(x / scale).
+ */
+#ifndef PAGEDATTN_H_
+#define PAGEDATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+#define PAGEDATTN_F16 0
+#define PAGEDATTN_BF16 1
+#define PAGEDATTN_E4M3 2 /* OCP float8 e4m3fn; KV pool only */
+#define PAGEDATTN_F32 3
+
+/* status codes */
+#define PAGEDATTN_OK 0
+#define PAGEDATTN_ERR_INVALID 1     /* bad argument / metadata */
+#define PAGEDATTN_ERR_UNSUPPORTED 2 /* shape or dtype not implemented */
+#define PAGEDATTN_ERR_WORKSPACE 3   /* workspace too small for the plan */
+#define PAGEDATTN_ERR_HIP 4         /* HIP runtime error (launch failure) */
+#define PAGEDATTN_ERR_PLAN 5        /* run does not match its plan */
+
+#define PAGEDATTN_ABI_VERSION 1
+
+/* Opaque host-side plan: the work partition built by a *_plan call and
+ * consumed by the matching *_run call.  One plan per wrapper object
+ * (src/models/llama.py:55-67); it is not thread-safe. */
+typedef struct pagedattn_plan pagedattn_plan;
+
+int pagedattn_abi_version(void);
+const char* pagedattn_last_error(void);
+
+/* Number of compute units of the current device (0 if no device). */
+int pagedattn_device_cu_count(void);
+
+/* ---------------------------------------------------------------------------
+ * flashinfer.get_batch_indices_positions(append_indptr, seq_lens, nnz)
+ * (called from src/models/llama.py:70-83 build_batch_indices_positions).
+ * For token j in [append_indptr[b], append_indptr[b+1]):
+ *   batch_indices[j] = b
+ *   positions[j]     = seq_lens[b] - (append_indptr[b+1]-append_indptr[b])
+ *                      + (j - append_indptr[b])
+ * append_indptr [batch_size+1], seq_lens [batch_size], outputs [nnz]; int32,
+ * device.  Entries of the outputs not covered by append_indptr are left as
+ * they are. */
+int pagedattn_get_batch_indices_positions(const int32_t* append_indptr,
+                                          const int32_t* seq_lens,
+                                          int32_t batch_size, int32_t nnz,
+                                          int32_t* batch_indices,
+                                          int32_t* positions, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * flashinfer.apply_rope_pos_ids_inplace(q, k, pos_ids, rotary_dim,
+ *     interleave, rope_scale, rope_theta)  (src/models/llama.py:175-182).
+ * q [nnz, num_qo_heads, head_dim], k [nnz, num_kv_heads, head_dim] (strided
+ * views of the fused qkv projection), rotated in place in fp32:
+ *   angle(i) = (pos / rope_scale) * rope_theta^(-2i/rotary_dim)
+ *   non-interleaved (rotate-half) pairs (i, i + rotary_dim/2), i < rotary_dim/2;
+ *   interleaved pairs (2i, 2i+1).
+ * Dimensions >= rotary_dim are left unchanged. dtype: F16 or BF16. */
+int pagedattn_apply_rope_pos_ids_inplace(
+    void* q, void* k, const int32_t* pos_ids, int32_t nnz,
+    int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t rotary_dim, int64_t q_stride_n, int64_t q_stride_h,
+    int64_t k_stride_n, int64_t k_stride_h, int32_t interleave,
+    float rope_scale, float rope_theta, int32_t dtype, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * flashinfer.append_paged_kv_cache(append_key, append_value, batch_indices,
+ *     positions, paged_kv_cache, kv_indices, kv_indptr, kv_last_page_len,
+ *     kv_layout="HND")  (src/models/llama.py:188-210).
+ * For token j: b = batch_indices[j], p = positions[j],
+ *   page = kv_indices[kv_indptr[b] + p / page_size], slot = p % page_size,
+ *   cache[page, 0, h, slot, :] = k[j, h, :];  cache[page, 1, h, slot, :] = v[j, h, :]
+ * Bit-exact copy when cache_dtype == src_dtype.  cache_dtype E4M3 stores
+ * round_to_nearest_even(clamp(x / scale, -448, 448)) with scale =
+ * kv_scales[(page*2 + {0,1})*num_kv_heads + h] (kv_scales may be NULL
+ * otherwise).  kv_last_page_len is accepted for interface parity and, as in
+ * the reference kernel, not used for addressing (may be NULL).
+ * Tokens whose batch index, page slot or page id fall outside the metadata
+ * are skipped and counted in *error_flag (int32, device; may be NULL). */
+int pagedattn_append_paged_kv_cache(
+    const void* append_key, const void* append_value, int64_t k_stride_n,
+    int64_t k_stride_h, int64_t v_stride_n, int64_t v_stride_h,
+    int32_t src_dtype, const int32_t* batch_indices, const int32_t* positions,
+    int32_t nnz, void* paged_kv_cache, int32_t cache_dtype,
+    const float* kv_scales, int32_t num_pages, const int32_t* kv_indices,
+    int32_t num_indices, const int32_t* kv_indptr,
+    const int32_t* kv_last_page_len, int32_t batch_size, int32_t num_kv_heads,
+    int32_t head_dim, int32_t page_size, int32_t* error_flag, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Plans.  pagedattn_plan_create/destroy manage the host object.
+ * BatchDecodeWithPagedKVCacheWrapper.begin_forward(kv_indptr, kv_indices,
+ *     kv_last_page_len, Hq, Hkv, D, page_size, q_data_type)
+ *     (src/models/llama.py:119-147).
+ * The metadata arrays are host copies.  split_pages > 0 forces split-KV
+ * chunks of that many pages (rounded up to a multiple of 8); 0 lets the
+ * planner choose from the device's CU count; -1 disables splitting.
+ * The work list and split partials are placed in `workspace` (device,
+ * workspace_bytes long) with one hipMemcpyAsync on `stream`. */
+pagedattn_plan* pagedattn_plan_create(void);
+void pagedattn_plan_destroy(pagedattn_plan* plan);
+
+int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
+                          const int32_t* kv_last_page_len_host,
+                          int32_t batch_size, int32_t num_qo_heads,
+                          int32_t num_kv_heads, int32_t head_dim,
+                          int32_t page_size, int32_t split_pages,
+                          void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* BatchDecodeWithPagedKVCacheWrapper.forward(q, paged_kv_cache)
+ * (src/models/llama.py:230-245).  q [batch, num_qo_heads, head_dim] strided;
+ * out [batch, num_qo_heads, head_dim] contiguous, q dtype; lse (optional,
+ * fp32 [batch, num_qo_heads], natural log of the softmax denominator of the
+ * scaled scores) may be NULL.  kv_scales is required for E4M3 pools. */
+int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
+                         int64_t q_stride_n, int64_t q_stride_h,
+                         int32_t q_dtype, const void* paged_kv_cache,
+                         int32_t kv_dtype, const float* kv_scales,
+                         int32_t num_pages, const int32_t* kv_indices,
+                         int32_t num_indices, const int32_t* kv_indptr,
+                         const int32_t* kv_last_page_len, void* out,
+                         float* lse, float sm_scale, void* stream);
+
+/* BatchPrefillWithPagedKVCacheWrapper.begin_forward(qo_indptr, kv_indptr,
+ *     kv_indices, kv_last_page_len, Hq, Hkv, D, page_size, q_data_type)
+ *     (src/models/llama.py:86-116).  Host copies of the indptr arrays. */
+int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
+                           const int32_t* kv_indptr_host,
+                           const int32_t* kv_last_page_len_host,
+                           int32_t batch_size, int32_t num_qo_heads,
+                           int32_t num_kv_heads, int32_t head_dim,
+                           int32_t page_size, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/* BatchPrefillWithPagedKVCacheWrapper.forward(q, paged_kv_cache, causal)
+ * (src/models/llama.py:212-228).  Ragged q [nnz, num_qo_heads, head_dim];
+ * with causal != 0, row i of sequence b sees kv token j iff
+ * j <= kv_len_b - qo_len_b + i (bottom-right aligned). */
+int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
+                          int64_t q_stride_n, int64_t q_stride_h,
+                          int32_t q_dtype, const int32_t* qo_indptr,
+                          const void* paged_kv_cache, int32_t kv_dtype,
+                          const float* kv_scales, int32_t num_pages,
+                          const int32_t* kv_indices, int32_t num_indices,
+                          const int32_t* kv_indptr,
+                          const int32_t* kv_last_page_len, void* out,
+                          float* lse, int32_t causal, float sm_scale,
+                          void* stream);
+
+/* ---------------------------------------------------------------------------
+ * No counterpart in the reference (its pool dtype equals the model dtype,
+ * src/engine/memory/allocator.py:34).  Builds an fp8 pool from a bf16/fp16
+ * pool: for every (page, K|V, kv-head) block, scale = amax / 448 (1.0 for an
+ * all-zero block) and dst = e4m3fn(round(src / scale)).
+ * src/dst [num_pages, 2, num_kv_heads, page_size, head_dim],
+ * scales [num_pages, 2, num_kv_heads] fp32. */
+int pagedattn_quantize_pages_e4m3(const void* src_cache, int32_t src_dtype,
+                                  void* dst_cache, float* scales,
+                                  int32_t num_pages, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t page_size,
+                                  void* stream);
+
+/* No counterpart in the reference: a plain streaming copy of `bytes` bytes
+ * (multiple of 16, 16-byte aligned pointers), used to calibrate HBM byte
+ * counters against a kernel of known traffic. */
+int pagedattn_copy_bytes(void* dst, const void* src, size_t bytes,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PAGEDATTN_H_ */

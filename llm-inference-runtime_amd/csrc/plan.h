@@ -1,0 +1,69 @@
+// Host plan object shared by the planner (plan.cpp) and the run launchers
+// (decode.hip, prefill.hip).  The plan is the work partition that
+// BatchDecode/BatchPrefillWithPagedKVCacheWrapper.begin_forward builds in the
+// reference (src/models/llama.py:86-147); the device copy of its work list
+// lives in the caller's workspace.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+#include "common.h"
+
+namespace pa {
+
+enum PlanMode { kPlanNone = 0, kPlanDecode = 1, kPlanPrefill = 2 };
+
+// One decode work item: pages [page_lo, page_hi) of sequence b for one KV
+// head (the head is blockIdx.y).  slot < 0 means the item covers the whole
+// sequence and writes the final output; otherwise it writes split partials
+// to `slot` and a merge item combines them.
+struct DecodeItem {
+  int32_t b, page_lo, page_hi, slot;
+};
+
+// Split-KV merge item: sequence b owns partial slots [slot0, slot0 + nslots).
+struct MergeItem {
+  int32_t b, slot0, nslots, pad;
+};
+
+// One prefill work item: query tokens [q_lo, q_hi) of sequence b (relative to
+// qo_indptr[b]) for one KV head and all its query heads; kv tokens
+// [kv_lo, kv_hi) of the causal/visible range (split-KV when slot >= 0).
+struct PrefillItem {
+  int32_t b, q_lo, q_hi, slot;
+};
+
+// Workspace layout: [0, kWsHeader) is reserved for the caller's device flags
+// (the Python shim keeps the append error counter at offset 0).
+constexpr size_t kWsHeader = 256;
+constexpr size_t kWsAlign = 256;
+
+inline size_t ws_align(size_t x) { return (x + kWsAlign - 1) & ~(kWsAlign - 1); }
+
+}  // namespace pa
+
+struct pagedattn_plan {
+  int mode = pa::kPlanNone;
+  int batch_size = 0, hq = 0, hkv = 0, d = 0, page_size = 0;
+  // decode
+  int n_items = 0, n_merge = 0, n_slots = 0, split_pages = 0;
+  // prefill: query tokens per tile (rows = tokens * hq/hkv)
+  int q_tile = 0;
+  int64_t total_qo = 0;
+  // device pointers into the workspace
+  void* items_dev = nullptr;
+  const int32_t* wg_ptr_dev = nullptr;  // decode: items of workgroup x
+  void* merge_dev = nullptr;
+  float* partial_o = nullptr;
+  float* partial_lse = nullptr;
+  void* workspace = nullptr;
+  size_t workspace_bytes = 0;
+  // host staging of the work lists (kept until the next plan so the async
+  // copy never reads freed memory)
+  std::vector<int32_t> host;
+  // statistics for the Python shim / tests
+  int64_t total_pages = 0;
+  int max_pages = 0;
+};

@@ -1,0 +1,33 @@
+"""MI355X (gfx950) paged attention for the mini-vLLM serving engine.
+
+``import pagedattn as flashinfer`` gives the engine's attention shim the
+FlashInfer entry points it uses; ``pagedattn.llama`` is a drop-in for the
+shim itself (src/models/llama.py).  All compute runs in libpagedattn.so;
+nothing here falls back to PyTorch.
+"""
+
+from .ops import (  # noqa: F401
+    PAGE_SIZE,
+    BatchDecodeWithPagedKVCacheWrapper,
+    BatchPrefillWithPagedKVCacheWrapper,
+    append_paged_kv_cache,
+    apply_rope_pos_ids_inplace,
+    copy_bytes,
+    get_batch_indices_positions,
+    quantize_pages_e4m3,
+)
+from ._lib import LIB_PATH, PagedAttnError, lib  # noqa: F401
+
+__all__ = [
+    "PAGE_SIZE",
+    "BatchDecodeWithPagedKVCacheWrapper",
+    "BatchPrefillWithPagedKVCacheWrapper",
+    "append_paged_kv_cache",
+    "apply_rope_pos_ids_inplace",
+    "copy_bytes",
+    "get_batch_indices_positions",
+    "quantize_pages_e4m3",
+    "LIB_PATH",
+    "PagedAttnError",
+    "lib",
+]

@@ -1,0 +1,144 @@
+"""ctypes binding of libpagedattn.so (the C ABI declared in include/pagedattn.h).
+
+The shared library is loaded after ``torch`` so that it binds to the HIP
+runtime torch already mapped (both carry the soname ``libamdhip64.so.7``):
+device pointers and ``hipStream_t`` handles from torch are then valid inside
+the library.  There is no fallback: if the library is missing, every entry
+point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+LIB_NAME = "libpagedattn.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+# element type codes (include/pagedattn.h)
+F16, BF16, E4M3, F32 = 0, 1, 2, 3
+
+_TORCH_TO_CODE = {
+    torch.float16: F16,
+    torch.bfloat16: BF16,
+    torch.float8_e4m3fn: E4M3,
+    torch.float32: F32,
+}
+
+ERR_NAMES = {
+    1: "invalid argument",
+    2: "unsupported",
+    3: "workspace too small",
+    4: "HIP error",
+    5: "plan mismatch",
+}
+
+_c_int = ctypes.c_int32
+_c_i64 = ctypes.c_int64
+_c_f = ctypes.c_float
+_c_p = ctypes.c_void_p
+_c_sz = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+_SIGNATURES = {
+    "pagedattn_abi_version": (_c_int, []),
+    "pagedattn_last_error": (ctypes.c_char_p, []),
+    "pagedattn_device_cu_count": (_c_int, []),
+    "pagedattn_get_batch_indices_positions": (
+        _c_int, [_c_p, _c_p, _c_int, _c_int, _c_p, _c_p, _c_p]),
+    "pagedattn_apply_rope_pos_ids_inplace": (
+        _c_int,
+        [_c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_f, _c_f, _c_int, _c_p]),
+    "pagedattn_append_paged_kv_cache": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p,
+         _c_int, _c_p, _c_int, _c_p, _c_int, _c_p, _c_int, _c_p, _c_p,
+         _c_int, _c_int, _c_int, _c_int, _c_p, _c_p]),
+    "pagedattn_plan_create": (_c_p, []),
+    "pagedattn_plan_destroy": (None, [_c_p]),
+    "pagedattn_decode_plan": (
+        _c_int,
+        [_c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_p, _c_sz, _c_p]),
+    "pagedattn_decode_run": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_int, _c_p, _c_int,
+         _c_p, _c_int, _c_p, _c_p, _c_p, _c_p, _c_f, _c_p]),
+    "pagedattn_prefill_plan": (
+        _c_int,
+        [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_p, _c_sz, _c_p]),
+    "pagedattn_prefill_run": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_int, _c_p, _c_int,
+         _c_p, _c_int, _c_p, _c_p, _c_p, _c_p, _c_int, _c_f, _c_p]),
+    "pagedattn_quantize_pages_e4m3": (
+        _c_int, [_c_p, _c_int, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_p]),
+    "pagedattn_copy_bytes": (_c_int, [_c_p, _c_p, _c_sz, _c_p]),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+
+_lib = None
+
+
+class PagedAttnError(RuntimeError):
+    """A libpagedattn entry point returned a non-zero status."""
+
+    def __init__(self, func: str, code: int, message: str):
+        super().__init__(f"{func}: {ERR_NAMES.get(code, code)}: {message}")
+        self.code = code
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the shared library; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run __graft_entry__.build() or "
+                "`make -C llm-inference-runtime_amd/csrc`")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call entry point `name`; raise PagedAttnError on a non-zero status."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().pagedattn_last_error()
+        raise PagedAttnError(name, rc, msg.decode() if msg else "")
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _TORCH_TO_CODE[dt]
+    except KeyError:
+        raise NotImplementedError(f"dtype {dt} is not supported") from None
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    """hipStream_t of torch's current stream on `device` (as an int)."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def loaded_hip_runtimes() -> list[str]:
+    """Paths of libamdhip64 mapped into this process (expected: exactly one)."""
+    paths = set()
+    with open("/proc/self/maps") as f:
+        for line in f:
+            if "libamdhip64" in line:
+                paths.add(line.split()[-1])
+    return sorted(paths)

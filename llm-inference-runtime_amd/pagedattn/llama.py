@@ -1,0 +1,226 @@
+"""Drop-in counterpart of the serving engine's attention shim
+(src/models/llama.py:1-382) running on the gfx950 paged-attention module.
+
+The engine imports exactly these names (src/engine/async_engine.py:21,
+src/engine/runtime/step_executor.py:8-13): ``FlashInferState``,
+``init_flashinfer_state``, ``build_batch_indices_positions``,
+``plan_prefill``, ``plan_decode`` and ``patch_llama_model``; the patched
+``LlamaAttention.forward`` keeps the reference's op order
+(qkv projection -> split -> RoPE -> page append -> attention -> o_proj).
+
+Deliberate differences from the reference:
+* RoPE theta/scaling are read from ``config.rope_parameters`` when present
+  (transformers >= 5 moved them there; the reference's
+  ``getattr(config, "rope_theta", 10000.0)`` at src/models/llama.py:346
+  silently falls back to 10000 for Llama-3).
+* bitsandbytes 4-bit projections (src/models/llama.py:283-336) are not fused
+  (bitsandbytes is CUDA-only); such a model raises NotImplementedError.
+* The pool may be e4m3 with ``FlashInferState.kv_scales`` [L, P, 2, Hkv].
+"""
+
+from __future__ import annotations
+
+from typing import cast
+
+import torch
+from torch import nn
+
+from . import ops
+
+
+class FlashInferState:
+    """Process-global state shared by all layers of one forward
+    (src/models/llama.py:16-36).  Attributes are writable from outside: the
+    decode step writes ``batch_indices``/``positions`` directly
+    (src/engine/runtime/step_executor.py:220-225)."""
+
+    kv_pool: torch.Tensor | None = None
+    kv_scales: torch.Tensor | None = None  # e4m3 pools only: [L, P, 2, Hkv]
+
+    kv_indices: torch.Tensor | None = None
+    kv_indptr: torch.Tensor | None = None
+    kv_last_page_len: torch.Tensor | None = None
+
+    batch_indices: torch.Tensor | None = None
+    positions: torch.Tensor | None = None
+
+    workspace_buffer: torch.Tensor | None = None
+
+    prefill_wrapper: ops.BatchPrefillWithPagedKVCacheWrapper | None = None
+    decode_wrapper: ops.BatchDecodeWithPagedKVCacheWrapper | None = None
+
+    page_size: int = 16
+    dtype: torch.dtype | None = None
+
+    mode: str = "prefill"
+
+
+WORKSPACE_BYTES = 128 * 1024 * 1024
+
+
+def init_flashinfer_state(*, kv_pool: torch.Tensor, page_size: int, device,
+                          kv_scales: torch.Tensor | None = None) -> None:
+    """Store the pool, allocate the 128 MiB workspace and the two wrappers
+    (src/models/llama.py:39-67)."""
+    if page_size != ops.PAGE_SIZE:
+        raise NotImplementedError(f"page_size {page_size} (only 16 is implemented)")
+    FlashInferState.kv_pool = kv_pool
+    FlashInferState.kv_scales = kv_scales
+    FlashInferState.page_size = page_size
+    FlashInferState.dtype = kv_pool.dtype
+    ws = torch.zeros(WORKSPACE_BYTES, dtype=torch.uint8, device=device)
+    FlashInferState.workspace_buffer = ws
+    FlashInferState.prefill_wrapper = ops.BatchPrefillWithPagedKVCacheWrapper(ws, "HND")
+    FlashInferState.decode_wrapper = ops.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+
+
+def append_error_count() -> int:
+    """Tokens the page append skipped because their metadata pointed outside
+    the page table since init (reads the device counter: synchronises)."""
+    ws = FlashInferState.workspace_buffer
+    if ws is None:
+        return 0
+    return int(ws[:4].view(torch.int32)[0].item())
+
+
+def build_batch_indices_positions(append_indptr: torch.Tensor, seq_lens: torch.Tensor) -> None:
+    """(src/models/llama.py:70-83)"""
+    nnz = int(append_indptr[-1].item())
+    FlashInferState.batch_indices, FlashInferState.positions = ops.get_batch_indices_positions(
+        append_indptr, seq_lens, nnz)
+
+
+def _q_dtype() -> torch.dtype:
+    dt = FlashInferState.dtype
+    # an e4m3 pool still runs bf16 queries
+    return torch.bfloat16 if dt == torch.float8_e4m3fn else cast(torch.dtype, dt)
+
+
+def plan_prefill(*, qo_indptr: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+                 kv_last_page_len: torch.Tensor, num_qo_heads: int, num_kv_heads: int,
+                 head_dim: int) -> None:
+    """(src/models/llama.py:86-116)"""
+    FlashInferState.mode = "prefill"
+    FlashInferState.kv_indptr = kv_indptr
+    FlashInferState.kv_indices = kv_indices
+    FlashInferState.kv_last_page_len = kv_last_page_len
+    pw = cast(ops.BatchPrefillWithPagedKVCacheWrapper, FlashInferState.prefill_wrapper)
+    pw.begin_forward(qo_indptr, kv_indptr, kv_indices, kv_last_page_len, num_qo_heads,
+                     num_kv_heads, head_dim, FlashInferState.page_size, q_data_type=_q_dtype())
+
+
+def plan_decode(*, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+                kv_last_page_len: torch.Tensor, num_qo_heads: int, num_kv_heads: int,
+                head_dim: int) -> None:
+    """(src/models/llama.py:119-147)"""
+    FlashInferState.mode = "decode"
+    FlashInferState.kv_indptr = kv_indptr
+    FlashInferState.kv_indices = kv_indices
+    FlashInferState.kv_last_page_len = kv_last_page_len
+    dw = cast(ops.BatchDecodeWithPagedKVCacheWrapper, FlashInferState.decode_wrapper)
+    dw.begin_forward(kv_indptr, kv_indices, kv_last_page_len, num_qo_heads, num_kv_heads,
+                     head_dim, FlashInferState.page_size, q_data_type=_q_dtype())
+
+
+def patched_llama_attention_forward(self, hidden_states: torch.Tensor,
+                                    position_embeddings=None, attention_mask=None,
+                                    past_key_value=None, output_attentions=False,
+                                    use_cache=False, cache_position=None, **kwargs):
+    """LlamaAttention.forward over the paged pool (src/models/llama.py:150-249).
+    Extra decoder kwargs (position_ids, past_key_values, ...) are ignored: the
+    positions come from FlashInferState."""
+    bsz, q_len, _ = hidden_states.shape
+    qkv = self.qkv_proj(hidden_states)
+    q, k, v = qkv.split([self.q_size, self.kv_size, self.kv_size], dim=-1)
+    q_rows = q.view(-1, self.num_heads, self.head_dim)
+    k_rows = k.view(-1, self.num_key_value_heads, self.head_dim)
+    v_rows = v.view(-1, self.num_key_value_heads, self.head_dim)
+
+    positions = cast(torch.Tensor, FlashInferState.positions)
+    ops.apply_rope_pos_ids_inplace(q_rows, k_rows, positions, rope_theta=self.rope_theta,
+                                   rope_scale=self.rope_scale, interleave=False)
+
+    pool = cast(torch.Tensor, FlashInferState.kv_pool)
+    layer_pool = pool[self.layer_idx]
+    scales = FlashInferState.kv_scales
+    layer_scales = scales[self.layer_idx] if scales is not None else None
+    ws = cast(torch.Tensor, FlashInferState.workspace_buffer)
+    ops.append_paged_kv_cache(
+        k_rows, v_rows, cast(torch.Tensor, FlashInferState.batch_indices), positions,
+        layer_pool, cast(torch.Tensor, FlashInferState.kv_indices),
+        cast(torch.Tensor, FlashInferState.kv_indptr),
+        cast(torch.Tensor, FlashInferState.kv_last_page_len), kv_layout="HND",
+        kv_scales=layer_scales, error_flag=ws[:4].view(torch.int32))
+
+    if FlashInferState.mode == "prefill":
+        pw = cast(ops.BatchPrefillWithPagedKVCacheWrapper, FlashInferState.prefill_wrapper)
+        out = pw.forward(q_rows, layer_pool, causal=True, kv_scales=layer_scales)
+        out = out.reshape(bsz, q_len, self.num_heads * self.head_dim)
+    else:
+        dw = cast(ops.BatchDecodeWithPagedKVCacheWrapper, FlashInferState.decode_wrapper)
+        out = dw.forward(q_rows, layer_pool, kv_scales=layer_scales)
+        out = out.reshape(bsz, 1, self.num_heads * self.head_dim)
+    return self.o_proj(out), None
+
+
+def _fuse_qkv_proj(attn) -> nn.Linear:
+    """One Linear whose output rows are q | k | v (src/models/llama.py:256-280)."""
+    parts = [attn.q_proj, attn.k_proj, attn.v_proj]
+    for p in parts:
+        if not isinstance(p, nn.Linear):
+            raise NotImplementedError(
+                f"{type(p).__name__} projections (e.g. bitsandbytes 4-bit) are not supported")
+    has_bias = any(p.bias is not None for p in parts)
+    w0 = attn.q_proj.weight
+    fused = nn.Linear(w0.shape[1], sum(p.weight.shape[0] for p in parts), bias=has_bias,
+                      device=w0.device, dtype=w0.dtype)
+    with torch.no_grad():
+        fused.weight.copy_(torch.cat([p.weight for p in parts], dim=0))
+        if has_bias:
+            fused.bias.copy_(torch.cat([
+                p.bias if p.bias is not None else torch.zeros(p.weight.shape[0], dtype=w0.dtype,
+                                                              device=w0.device)
+                for p in parts]))
+    return fused
+
+
+def rope_config(config) -> tuple[float, float]:
+    """(rope_theta, linear rope_scale) of a Llama config; rejects scaling
+    types that a single linear factor cannot express (src/models/llama.py:346-361)."""
+    params = getattr(config, "rope_parameters", None)
+    if isinstance(params, dict) and params:
+        theta = float(params.get("rope_theta", getattr(config, "rope_theta", 10000.0)))
+        scaling = params
+    else:
+        theta = float(getattr(config, "rope_theta", 10000.0))
+        scaling = getattr(config, "rope_scaling", None)
+    scale = 1.0
+    if scaling:
+        rope_type = scaling.get("rope_type", scaling.get("type"))
+        if rope_type not in (None, "default", "linear"):
+            raise NotImplementedError(
+                f"rope scaling type {rope_type!r} is not a linear position scale")
+        if rope_type == "linear":
+            scale = float(scaling.get("factor", 1.0))
+    return theta, scale
+
+
+def patch_llama_model(model) -> None:
+    """Install the paged forward on every decoder layer (src/models/llama.py:345-382)."""
+    from transformers.models.llama.modeling_llama import LlamaAttention
+
+    cfg = model.config
+    theta, scale = rope_config(cfg)
+    for idx, layer in enumerate(model.model.layers):
+        attn = layer.self_attn
+        attn.layer_idx = idx
+        attn.num_heads = cfg.num_attention_heads
+        attn.num_key_value_heads = cfg.num_key_value_heads
+        attn.head_dim = cfg.hidden_size // cfg.num_attention_heads
+        attn.q_size = attn.num_heads * attn.head_dim
+        attn.kv_size = attn.num_key_value_heads * attn.head_dim
+        attn.rope_theta = theta
+        attn.rope_scale = scale
+        attn.qkv_proj = _fuse_qkv_proj(attn)
+        del attn.q_proj, attn.k_proj, attn.v_proj
+        attn.forward = patched_llama_attention_forward.__get__(attn, LlamaAttention)

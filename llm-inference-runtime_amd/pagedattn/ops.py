@@ -1,0 +1,438 @@
+"""FlashInfer-compatible Python surface over libpagedattn.
+
+These are the FlashInfer entry points the serving engine calls on its
+attention path (src/models/llama.py:3, :49-67, :79-83, :106-116, :138-147,
+:175-182, :188-210, :218-222, :236-239), with the same names, argument
+meaning and error behaviour (Python exceptions, never a device fault):
+
+* ``get_batch_indices_positions``
+* ``apply_rope_pos_ids_inplace``
+* ``append_paged_kv_cache``
+* ``BatchDecodeWithPagedKVCacheWrapper`` (``plan``/``begin_forward``,
+  ``run``/``forward``)
+* ``BatchPrefillWithPagedKVCacheWrapper`` (same)
+
+Only the "HND" pool layout the engine uses is implemented
+([num_pages, 2, num_kv_heads, page_size, head_dim] per layer).  Options the
+engine never passes (positional encoding inside attention, sliding windows,
+logit soft-capping, custom masks) raise NotImplementedError.
+
+Additions with no FlashInfer counterpart: ``quantize_pages_e4m3`` and the
+``kv_scales`` argument for e4m3 pools with per-(page, K|V, kv-head) scales.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from ._lib import call, dtype_code, ptr
+
+PAGE_SIZE = 16
+
+
+def _dtype_of(x) -> torch.dtype:
+    if isinstance(x, torch.dtype):
+        return x
+    if isinstance(x, str):
+        return getattr(torch, x)
+    raise TypeError(f"not a dtype: {x!r}")
+
+
+def _require_cuda(t: torch.Tensor, name: str) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name} must be a device (cuda/hip) tensor, got {t.device}")
+
+
+def _i32(t: torch.Tensor, device: torch.device) -> torch.Tensor:
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def _host_i32(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().to("cpu", torch.int32).contiguous()
+
+
+def _stream(device: torch.device) -> int:
+    return _lib.stream_of(device)
+
+
+def _check_pool(paged_kv_cache, num_kv_heads: int | None, head_dim: int | None,
+                kv_layout: str) -> tuple[int, int, int]:
+    if kv_layout != "HND":
+        raise NotImplementedError(
+            f"kv_layout {kv_layout!r}: only the HND page layout is implemented")
+    if isinstance(paged_kv_cache, (tuple, list)):
+        raise NotImplementedError(
+            "separate (k_cache, v_cache) tensors are not supported; pass the "
+            "[num_pages, 2, num_kv_heads, page_size, head_dim] layer pool")
+    _require_cuda(paged_kv_cache, "paged_kv_cache")
+    if paged_kv_cache.dim() != 5 or paged_kv_cache.shape[1] != 2:
+        raise ValueError(
+            "paged_kv_cache must be [num_pages, 2, num_kv_heads, page_size, "
+            f"head_dim], got {tuple(paged_kv_cache.shape)}")
+    p, _, hkv, page, d = paged_kv_cache.shape
+    if page != PAGE_SIZE:
+        raise NotImplementedError(f"page_size {page} (only 16 is implemented)")
+    if num_kv_heads is not None and hkv != num_kv_heads:
+        raise ValueError(f"pool has {hkv} kv heads, plan says {num_kv_heads}")
+    if head_dim is not None and d != head_dim:
+        raise ValueError(f"pool head_dim {d}, plan says {head_dim}")
+    if not paged_kv_cache.is_contiguous():
+        raise ValueError("paged_kv_cache (one layer of the pool) must be contiguous")
+    return p, hkv, d
+
+
+def _check_scales(kv_scales, paged_kv_cache) -> torch.Tensor | None:
+    if paged_kv_cache.dtype != torch.float8_e4m3fn:
+        return None
+    if kv_scales is None:
+        raise ValueError("an e4m3 pool needs kv_scales [num_pages, 2, num_kv_heads]")
+    p, _, hkv, _, _ = paged_kv_cache.shape
+    if kv_scales.dtype != torch.float32 or tuple(kv_scales.shape) != (p, 2, hkv):
+        raise ValueError(
+            f"kv_scales must be float32 [{p}, 2, {hkv}], got "
+            f"{kv_scales.dtype} {tuple(kv_scales.shape)}")
+    _require_cuda(kv_scales, "kv_scales")
+    return kv_scales.contiguous()
+
+
+def _check_rows(x: torch.Tensor, name: str, heads: int | None, d: int | None):
+    _require_cuda(x, name)
+    if x.dim() != 3:
+        raise ValueError(f"{name} must be [tokens, heads, head_dim], got {tuple(x.shape)}")
+    if heads is not None and x.shape[1] != heads:
+        raise ValueError(f"{name} has {x.shape[1]} heads, expected {heads}")
+    if d is not None and x.shape[2] != d:
+        raise ValueError(f"{name} head_dim {x.shape[2]}, expected {d}")
+    if x.shape[0] > 0 and x.stride(2) != 1:
+        raise ValueError(f"{name}: the head_dim axis must be contiguous")
+
+
+# -----------------------------------------------------------------------------
+def get_batch_indices_positions(append_indptr: torch.Tensor, seq_lens: torch.Tensor,
+                                nnz: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """batch_indices[j] = b and positions[j] = seq_lens[b] - append_len_b + (j - append_indptr[b])
+    for j in [append_indptr[b], append_indptr[b+1]) (src/models/llama.py:70-83)."""
+    _require_cuda(append_indptr, "append_indptr")
+    device = append_indptr.device
+    indptr = _i32(append_indptr, device)
+    lens = _i32(seq_lens, device)
+    bsz = lens.numel()
+    if indptr.numel() != bsz + 1:
+        raise ValueError(f"append_indptr has {indptr.numel()} entries for {bsz} sequences")
+    nnz = int(nnz)
+    bi = torch.empty(nnz, dtype=torch.int32, device=device)
+    pos = torch.empty(nnz, dtype=torch.int32, device=device)
+    call("pagedattn_get_batch_indices_positions", ptr(indptr), ptr(lens), bsz, nnz,
+         ptr(bi), ptr(pos), _stream(device))
+    return bi, pos
+
+
+def apply_rope_pos_ids_inplace(q: torch.Tensor, k: torch.Tensor, pos_ids: torch.Tensor,
+                               rotary_dim: int | None = None, interleave: bool = False,
+                               rope_scale: float = 1.0, rope_theta: float = 1e4) -> None:
+    """RoPE in place on q [nnz, Hq, D] and k [nnz, Hkv, D] (src/models/llama.py:175-182)."""
+    _check_rows(q, "q", None, None)
+    _check_rows(k, "k", None, q.shape[2])
+    if q.dtype != k.dtype:
+        raise ValueError("q and k must share a dtype")
+    if k.shape[0] != q.shape[0] or pos_ids.numel() != q.shape[0]:
+        raise ValueError("q, k and pos_ids must have the same number of tokens")
+    nnz, hq, d = q.shape
+    hkv = k.shape[1]
+    pos = _i32(pos_ids, q.device)
+    call("pagedattn_apply_rope_pos_ids_inplace", ptr(q), ptr(k), ptr(pos), nnz, hq, hkv, d,
+         int(rotary_dim or d), q.stride(0), q.stride(1), k.stride(0), k.stride(1),
+         int(bool(interleave)), float(rope_scale), float(rope_theta), dtype_code(q.dtype),
+         _stream(q.device))
+
+
+def append_paged_kv_cache(append_key: torch.Tensor, append_value: torch.Tensor,
+                          batch_indices: torch.Tensor, positions: torch.Tensor,
+                          paged_kv_cache: torch.Tensor, kv_indices: torch.Tensor,
+                          kv_indptr: torch.Tensor, kv_last_page_len: torch.Tensor,
+                          kv_layout: str = "NHD", kv_scales: torch.Tensor | None = None,
+                          error_flag: torch.Tensor | None = None) -> None:
+    """Scatter k/v rows into their pages (src/models/llama.py:188-210).
+
+    Bit-exact for a pool of the source dtype; an e4m3 pool stores
+    round(clamp(x / scale, +-448)) with kv_scales [num_pages, 2, Hkv].
+    `error_flag` (int32 device scalar, optional) counts tokens whose metadata
+    pointed outside the page table; those tokens are skipped."""
+    num_pages, hkv, d = _check_pool(paged_kv_cache, None, None, kv_layout)
+    _check_rows(append_key, "append_key", hkv, d)
+    _check_rows(append_value, "append_value", hkv, d)
+    if append_key.dtype != append_value.dtype:
+        raise ValueError("append_key and append_value must share a dtype")
+    nnz = append_key.shape[0]
+    if append_value.shape[0] != nnz or batch_indices.numel() != nnz or positions.numel() != nnz:
+        raise ValueError("append_key/value, batch_indices and positions disagree on nnz")
+    scales = _check_scales(kv_scales, paged_kv_cache)
+    if paged_kv_cache.dtype not in (append_key.dtype, torch.float8_e4m3fn):
+        raise ValueError(f"pool dtype {paged_kv_cache.dtype} cannot take {append_key.dtype} rows")
+    device = paged_kv_cache.device
+    bi = _i32(batch_indices, device)
+    pos = _i32(positions, device)
+    ind = _i32(kv_indices, device)
+    indptr = _i32(kv_indptr, device)
+    bsz = indptr.numel() - 1
+    if error_flag is not None and (error_flag.dtype != torch.int32 or error_flag.numel() < 1):
+        raise ValueError("error_flag must be an int32 device tensor")
+    call("pagedattn_append_paged_kv_cache", ptr(append_key), ptr(append_value),
+         append_key.stride(0), append_key.stride(1), append_value.stride(0),
+         append_value.stride(1), dtype_code(append_key.dtype), ptr(bi), ptr(pos), nnz,
+         ptr(paged_kv_cache), dtype_code(paged_kv_cache.dtype), ptr(scales), num_pages,
+         ptr(ind), ind.numel(), ptr(indptr), ptr(kv_last_page_len), bsz, hkv, d, PAGE_SIZE,
+         ptr(error_flag), _stream(device))
+
+
+def quantize_pages_e4m3(pool: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """bf16/fp16 layer pool -> (e4m3 pool, fp32 scales [P, 2, Hkv]) with
+    scale = amax / 448 per (page, K|V, kv-head) block (1.0 for an all-zero block)."""
+    num_pages, hkv, d = _check_pool(pool, None, None, "HND")
+    out = torch.empty(pool.shape, dtype=torch.float8_e4m3fn, device=pool.device)
+    scales = torch.empty((num_pages, 2, hkv), dtype=torch.float32, device=pool.device)
+    call("pagedattn_quantize_pages_e4m3", ptr(pool), dtype_code(pool.dtype), ptr(out),
+         ptr(scales), num_pages, hkv, d, PAGE_SIZE, _stream(pool.device))
+    return out, scales
+
+
+def copy_bytes(dst: torch.Tensor, src: torch.Tensor) -> None:
+    """Plain 16-byte streaming copy (HBM counter calibration)."""
+    n = src.numel() * src.element_size()
+    if dst.numel() * dst.element_size() < n:
+        raise ValueError("dst smaller than src")
+    call("pagedattn_copy_bytes", ptr(dst), ptr(src), n, _stream(src.device))
+
+
+# -----------------------------------------------------------------------------
+class _Plan:
+    """Owns one host plan object of the library."""
+
+    def __init__(self):
+        self.handle = _lib.lib().pagedattn_plan_create()
+        if not self.handle:
+            raise MemoryError("pagedattn_plan_create failed")
+
+    def __del__(self):
+        h = getattr(self, "handle", None)
+        if h and _lib._lib is not None:
+            _lib._lib.pagedattn_plan_destroy(h)
+            self.handle = None
+
+
+def _unsupported_options(pos_encoding_mode="NONE", window_left=-1, logits_soft_cap=None,
+                         custom_mask=None, packed_custom_mask=None) -> None:
+    if pos_encoding_mode not in ("NONE", None):
+        raise NotImplementedError(
+            f"pos_encoding_mode={pos_encoding_mode!r}: RoPE is applied by "
+            "apply_rope_pos_ids_inplace before attention")
+    if window_left not in (-1, None):
+        raise NotImplementedError("sliding-window attention is not implemented")
+    if logits_soft_cap not in (None, 0, 0.0):
+        raise NotImplementedError("logits_soft_cap is not implemented")
+    if custom_mask is not None or packed_custom_mask is not None:
+        raise NotImplementedError("custom masks are not implemented")
+
+
+class _WrapperBase:
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 use_cuda_graph: bool = False, **_unused):
+        if kv_layout != "HND":
+            raise NotImplementedError(
+                f"kv_layout {kv_layout!r}: only the HND page layout is implemented")
+        if use_cuda_graph:
+            raise NotImplementedError("use_cuda_graph wrappers are not implemented")
+        _require_cuda(float_workspace_buffer, "float_workspace_buffer")
+        if not float_workspace_buffer.is_contiguous():
+            raise ValueError("the workspace must be contiguous")
+        self._ws = float_workspace_buffer
+        self._kv_layout = kv_layout
+        self._plan = _Plan()
+        self._planned = False
+
+    @property
+    def _ws_bytes(self) -> int:
+        return self._ws.numel() * self._ws.element_size()
+
+    def reset_workspace_buffer(self, float_workspace_buffer: torch.Tensor, *_a) -> None:
+        self._ws = float_workspace_buffer
+        self._planned = False
+
+    def end_forward(self) -> None:
+        """Kept for interface parity; the plan needs no teardown."""
+
+
+class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
+    """Paged decode attention: one query token per sequence over its whole
+    paged KV, GQA, no mask (src/models/llama.py:62-67, :119-147, :230-245).
+
+    Long sequences are split into KV chunks whose partials are merged by
+    log-sum-exp; `plan(..., split_pages=n)` fixes the chunk size (pages),
+    0 lets the planner balance the work over the GPU, -1 disables splitting."""
+
+    def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
+             num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
+             pos_encoding_mode: str = "NONE", window_left: int = -1,
+             logits_soft_cap: float | None = None, q_data_type="float16",
+             kv_data_type=None, data_type=None, sm_scale: float | None = None,
+             rope_scale=None, rope_theta=None, non_blocking: bool = True,
+             split_pages: int = 0, **_unused) -> None:
+        _unsupported_options(pos_encoding_mode, window_left, logits_soft_cap)
+        if page_size != PAGE_SIZE:
+            raise NotImplementedError(f"page_size {page_size} (only 16 is implemented)")
+        device = self._ws.device
+        indptr_h = _host_i32(indptr)
+        last_h = _host_i32(last_page_len)
+        bsz = last_h.numel()
+        if indptr_h.numel() != bsz + 1:
+            raise ValueError(f"indptr has {indptr_h.numel()} entries for {bsz} sequences")
+        n_ind = int(indptr_h[-1]) if bsz else 0
+        if indices.numel() < n_ind:
+            raise ValueError(f"indices has {indices.numel()} entries, indptr needs {n_ind}")
+        self._q_dtype = _dtype_of(data_type if data_type is not None else q_data_type)
+        self._kv_dtype = _dtype_of(kv_data_type) if kv_data_type is not None else None
+        call("pagedattn_decode_plan", self._plan.handle, ptr(indptr_h), ptr(last_h), bsz,
+             int(num_qo_heads), int(num_kv_heads), int(head_dim), int(page_size),
+             int(split_pages), ptr(self._ws), self._ws_bytes, _stream(device))
+        self._indptr = _i32(indptr, device)
+        self._indices = _i32(indices, device)
+        self._last = _i32(last_page_len, device)
+        self._bsz, self._hq, self._hkv, self._d = bsz, int(num_qo_heads), int(num_kv_heads), int(head_dim)
+        self._sm_scale = sm_scale
+        self._planned = True
+
+    begin_forward = plan
+
+    def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, *,
+            kv_scales: torch.Tensor | None = None, out: torch.Tensor | None = None,
+            lse: torch.Tensor | None = None, return_lse: bool = False,
+            sm_scale: float | None = None):
+        if not self._planned:
+            raise RuntimeError("plan()/begin_forward() must be called before run()/forward()")
+        num_pages, _, _ = _check_pool(paged_kv_cache, self._hkv, self._d, self._kv_layout)
+        _check_rows(q, "q", self._hq, self._d)
+        if q.shape[0] != self._bsz:
+            raise ValueError(f"q has {q.shape[0]} rows, the plan has {self._bsz} sequences")
+        if q.dtype not in (torch.float16, torch.bfloat16):
+            raise NotImplementedError(f"q dtype {q.dtype}")
+        scales = _check_scales(kv_scales, paged_kv_cache)
+        if out is None:
+            out = torch.empty((self._bsz, self._hq, self._d), dtype=q.dtype, device=q.device)
+        elif not out.is_contiguous() or tuple(out.shape) != (self._bsz, self._hq, self._d):
+            raise ValueError("out must be a contiguous [batch, num_qo_heads, head_dim] tensor")
+        if return_lse and lse is None:
+            lse = torch.empty((self._bsz, self._hq), dtype=torch.float32, device=q.device)
+        scale = sm_scale if sm_scale is not None else self._sm_scale
+        if scale is None:
+            scale = 1.0 / math.sqrt(self._d)
+        call("pagedattn_decode_run", self._plan.handle, ptr(q), q.stride(0), q.stride(1),
+             dtype_code(q.dtype), ptr(paged_kv_cache), dtype_code(paged_kv_cache.dtype),
+             ptr(scales), num_pages, ptr(self._indices), self._indices.numel(),
+             ptr(self._indptr), ptr(self._last), ptr(out), ptr(lse), float(scale),
+             _stream(q.device))
+        return (out, lse) if return_lse else out
+
+    def forward(self, q: torch.Tensor, paged_kv_cache: torch.Tensor,
+                pos_encoding_mode: str = "NONE", q_scale=None, k_scale=None, v_scale=None,
+                window_left: int = -1, logits_soft_cap: float | None = None,
+                sm_scale: float | None = None, rope_scale=None, rope_theta=None,
+                return_lse: bool = False, kv_scales: torch.Tensor | None = None):
+        _unsupported_options(pos_encoding_mode, window_left, logits_soft_cap)
+        if q_scale is not None or k_scale is not None or v_scale is not None:
+            raise NotImplementedError("scalar q/k/v scales; pass per-page kv_scales")
+        return self.run(q, paged_kv_cache, kv_scales=kv_scales, return_lse=return_lse,
+                        sm_scale=sm_scale)
+
+
+class BatchPrefillWithPagedKVCacheWrapper(_WrapperBase):
+    """Ragged-query, paged-KV attention with GQA and a bottom-right aligned
+    causal mask (src/models/llama.py:55-60, :86-116, :212-228): row i of
+    sequence b sees kv token j iff j <= kv_len_b - qo_len_b + i."""
+
+    def plan(self, qo_indptr: torch.Tensor, paged_kv_indptr: torch.Tensor,
+             paged_kv_indices: torch.Tensor, paged_kv_last_page_len: torch.Tensor,
+             num_qo_heads: int, num_kv_heads: int, head_dim_qk: int, page_size: int,
+             head_dim_vo: int | None = None, custom_mask=None, packed_custom_mask=None,
+             causal: bool = False, pos_encoding_mode: str = "NONE",
+             window_left: int = -1, logits_soft_cap: float | None = None,
+             q_data_type="float16", kv_data_type=None, sm_scale: float | None = None,
+             rope_scale=None, rope_theta=None, non_blocking: bool = True,
+             **_unused) -> None:
+        _unsupported_options(pos_encoding_mode, window_left, logits_soft_cap, custom_mask,
+                             packed_custom_mask)
+        if head_dim_vo is not None and head_dim_vo != head_dim_qk:
+            raise NotImplementedError("head_dim_vo != head_dim_qk")
+        if page_size != PAGE_SIZE:
+            raise NotImplementedError(f"page_size {page_size} (only 16 is implemented)")
+        device = self._ws.device
+        qo_h = _host_i32(qo_indptr)
+        indptr_h = _host_i32(paged_kv_indptr)
+        last_h = _host_i32(paged_kv_last_page_len)
+        bsz = last_h.numel()
+        if qo_h.numel() != bsz + 1 or indptr_h.numel() != bsz + 1:
+            raise ValueError("qo_indptr and paged_kv_indptr need batch_size + 1 entries")
+        n_ind = int(indptr_h[-1]) if bsz else 0
+        if paged_kv_indices.numel() < n_ind:
+            raise ValueError(
+                f"paged_kv_indices has {paged_kv_indices.numel()} entries, indptr needs {n_ind}")
+        self._q_dtype = _dtype_of(q_data_type)
+        call("pagedattn_prefill_plan", self._plan.handle, ptr(qo_h), ptr(indptr_h),
+             ptr(last_h), bsz, int(num_qo_heads), int(num_kv_heads), int(head_dim_qk),
+             int(page_size), ptr(self._ws), self._ws_bytes, _stream(device))
+        self._qo_indptr = _i32(qo_indptr, device)
+        self._qo_rows = int(qo_h[-1]) if bsz else 0
+        self._indptr = _i32(paged_kv_indptr, device)
+        self._indices = _i32(paged_kv_indices, device)
+        self._last = _i32(paged_kv_last_page_len, device)
+        self._bsz, self._hq, self._hkv, self._d = (bsz, int(num_qo_heads), int(num_kv_heads),
+                                                   int(head_dim_qk))
+        self._causal = bool(causal)
+        self._sm_scale = sm_scale
+        self._planned = True
+
+    begin_forward = plan
+
+    def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, *,
+            kv_scales: torch.Tensor | None = None, out: torch.Tensor | None = None,
+            lse: torch.Tensor | None = None, return_lse: bool = False,
+            causal: bool | None = None, sm_scale: float | None = None):
+        if not self._planned:
+            raise RuntimeError("plan()/begin_forward() must be called before run()/forward()")
+        num_pages, _, _ = _check_pool(paged_kv_cache, self._hkv, self._d, self._kv_layout)
+        _check_rows(q, "q", self._hq, self._d)
+        if q.shape[0] < self._qo_rows:
+            raise ValueError(f"q has {q.shape[0]} rows, qo_indptr needs {self._qo_rows}")
+        if q.dtype not in (torch.float16, torch.bfloat16):
+            raise NotImplementedError(f"q dtype {q.dtype}")
+        scales = _check_scales(kv_scales, paged_kv_cache)
+        n = q.shape[0]
+        if out is None:
+            out = torch.empty((n, self._hq, self._d), dtype=q.dtype, device=q.device)
+        elif not out.is_contiguous() or tuple(out.shape) != (n, self._hq, self._d):
+            raise ValueError("out must be a contiguous [nnz, num_qo_heads, head_dim] tensor")
+        if return_lse and lse is None:
+            lse = torch.empty((n, self._hq), dtype=torch.float32, device=q.device)
+        scale = sm_scale if sm_scale is not None else self._sm_scale
+        if scale is None:
+            scale = 1.0 / math.sqrt(self._d)
+        is_causal = self._causal if causal is None else bool(causal)
+        call("pagedattn_prefill_run", self._plan.handle, ptr(q), q.stride(0), q.stride(1),
+             dtype_code(q.dtype), ptr(self._qo_indptr), ptr(paged_kv_cache),
+             dtype_code(paged_kv_cache.dtype), ptr(scales), num_pages, ptr(self._indices),
+             self._indices.numel(), ptr(self._indptr), ptr(self._last), ptr(out), ptr(lse),
+             int(is_causal), float(scale), _stream(q.device))
+        return (out, lse) if return_lse else out
+
+    def forward(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, causal: bool = False,
+                pos_encoding_mode: str = "NONE", window_left: int = -1,
+                logits_soft_cap: float | None = None, sm_scale: float | None = None,
+                rope_scale=None, rope_theta=None, return_lse: bool = False,
+                kv_scales: torch.Tensor | None = None, **_unused):
+        _unsupported_options(pos_encoding_mode, window_left, logits_soft_cap)
+        return self.run(q, paged_kv_cache, kv_scales=kv_scales, return_lse=return_lse,
+                        causal=causal, sm_scale=sm_scale)

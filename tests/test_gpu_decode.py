@@ -1,0 +1,161 @@
+"""GPU parity of paged decode attention (bf16/fp16 and e4m3 pools) against the
+fp32 CPU oracle: max-abs 2e-2 for bf16/fp16 outputs, 3e-2 for e4m3 pools,
+log-sum-exp within 2e-3.  Full-size workloads add size-independent checks:
+every split-KV partition must give the same output."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+import pagedattn
+from pagedattn import workloads as W
+from pagedattn.metadata import decode_metadata
+
+from paged_cases import (decode_case, i32, lse_err, max_err, oracle_decode, random_tables,
+                         run_decode, workspace)
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 2e-2
+TOL_FP8 = 3e-2
+TOL_LSE = 2e-3
+
+EDGE_LENS = [1, 2, 15, 16, 17, 31, 32, 33, 47, 48, 64, 100, 255, 256, 257, 700]
+
+
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (32, 8), (8, 8), (16, 8), (32, 2), (64, 8)])
+def test_decode_edge_lengths(gpu, d, hq, hkv):
+    meta, pool, q = decode_case(gpu, EDGE_LENS, hq, hkv, d, seed=hq + hkv + d)
+    ref_o, ref_l = oracle_decode(meta, pool, q)
+    for split in (-1, 0, 8):
+        out, lse = run_decode(gpu, meta, pool, q, hq, hkv, d, split_pages=split)
+        assert max_err(out, ref_o) <= TOL_BF16, (split, max_err(out, ref_o))
+        assert lse_err(lse, ref_l) <= TOL_LSE, split
+
+
+def test_decode_fp16(gpu):
+    meta, pool, q = decode_case(gpu, EDGE_LENS, 32, 4, 64, dtype=torch.float16, seed=11)
+    ref_o, ref_l = oracle_decode(meta, pool, q)
+    out, lse = run_decode(gpu, meta, pool, q, 32, 4, 64)
+    assert out.dtype == torch.float16
+    assert max_err(out, ref_o) <= TOL_BF16
+    assert lse_err(lse, ref_l) <= TOL_LSE
+
+
+def test_decode_empty_and_single_sequences(gpu):
+    # a sequence with no pages gets zeros and lse = -inf; B = 1 works
+    d, hq, hkv = 64, 32, 4
+    from types import SimpleNamespace
+    meta = SimpleNamespace(kv_indptr=np.array([0, 3, 3, 4], np.int32),
+                           kv_indices=np.array([6, 2, 0, 4], np.int32),
+                           kv_last_page_len=np.array([8, 1, 5], np.int32))
+    num_pages = 8
+    g = torch.Generator(device=gpu)
+    g.manual_seed(1)
+    pool = torch.randn((num_pages, 2, hkv, 16, d), generator=g, device=gpu).to(torch.bfloat16)
+    q = torch.randn((3, hq, d), generator=g, device=gpu).to(torch.bfloat16)
+    ref_o, ref_l = oracle_decode(meta, pool, q)
+    out, lse = run_decode(gpu, meta, pool, q, hq, hkv, d)
+    assert torch.equal(out[1].float().cpu(), torch.zeros(hq, d))
+    assert bool(torch.isinf(lse[1]).all())
+    assert max_err(out, ref_o) <= TOL_BF16
+    assert lse_err(lse, ref_l) <= TOL_LSE
+    meta1, pool1, q1 = decode_case(gpu, [333], hq, hkv, d, seed=3)
+    o1, _ = run_decode(gpu, meta1, pool1, q1, hq, hkv, d)
+    assert max_err(o1, oracle_decode(meta1, pool1, q1)[0]) <= TOL_BF16
+
+
+def test_decode_bad_page_ids_do_not_fault(gpu):
+    # out-of-range page ids read as empty pages (no fault); other rows stay exact
+    meta, pool, q = decode_case(gpu, [40, 40, 40], 32, 4, 64, seed=4)
+    bad = meta.kv_indices.copy()
+    bad[meta.kv_indptr[1]] = pool.shape[0] + 1000
+    ws = workspace(gpu)
+    w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    w.plan(i32(meta.kv_indptr, gpu), i32(bad, gpu), i32(meta.kv_last_page_len, gpu), 32, 4, 64,
+           16, q_data_type=torch.bfloat16)
+    out = w.run(q, pool)
+    ref_o, _ = oracle_decode(meta, pool, q)
+    assert torch.isfinite(out.float()).all()
+    assert max_err(out, ref_o, rows=[0, 2]) <= TOL_BF16
+
+
+def _fused_append_then_decode(gpu, w, t, split_pages=None, ws=None):
+    m = w.meta
+    pagedattn.append_paged_kv_cache(t.k_new, t.v_new, t.batch_indices, t.positions, t.pool,
+                                    t.kv_indices, t.kv_indptr, t.kv_last_page_len,
+                                    kv_layout="HND", kv_scales=t.scales)
+    ws = workspace(gpu) if ws is None else ws
+    dw = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    dw.plan(t.kv_indptr, t.kv_indices, t.kv_last_page_len, w.hq, w.hkv, w.d, 16,
+            q_data_type=t.q.dtype,
+            split_pages=w.split_pages if split_pages is None else split_pages)
+    out, lse = dw.run(t.q, t.pool, kv_scales=t.scales, return_lse=True)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def test_decode_tinyllama_small(gpu):
+    w = W.tinyllama_decode_small(seed=0)
+    t = W.materialize(w, gpu)
+    before = O.to_bits(t.pool)
+    out, lse = _fused_append_then_decode(gpu, w, t)
+    m = w.meta
+    want, _ = O.append_pages(before, O.to_bits(t.k_new), O.to_bits(t.v_new), m.batch_indices,
+                             m.positions, m.kv_indices, m.kv_indptr)
+    assert np.array_equal(O.to_bits(t.pool), want)
+    ref_o, ref_l = oracle_decode(m, t.pool, t.q)
+    assert max_err(out, ref_o) <= TOL_BF16
+    assert lse_err(lse, ref_l) <= TOL_LSE
+
+
+def test_decode_tinyllama_at_scale(gpu):
+    w = W.tinyllama_decode(seed=0)
+    t = W.materialize(w, gpu)
+    out, lse = _fused_append_then_decode(gpu, w, t)
+    ref_o, ref_l = oracle_decode(w.meta, t.pool, t.q)
+    assert max_err(out, ref_o) <= TOL_BF16
+    assert lse_err(lse, ref_l) <= TOL_LSE
+    # size-independent: every split-KV partition gives the same answer
+    ws = workspace(gpu)
+    for split in (-1, 8, 40):
+        dw = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+        dw.plan(t.kv_indptr, t.kv_indices, t.kv_last_page_len, w.hq, w.hkv, w.d, 16,
+                q_data_type=t.q.dtype, split_pages=split)
+        o2 = dw.run(t.q, t.pool)
+        assert float((o2.float() - out.float()).abs().max()) <= 1e-2, split
+
+
+def test_decode_long_context_split(gpu):
+    # full-size long-context batch; oracle on a seeded subset of sequences,
+    # all sequences through the split-invariance property
+    w = W.llama3_8b_long_decode(seed=0)
+    t = W.materialize(w, gpu)
+    out, lse = _fused_append_then_decode(gpu, w, t)  # 4096-token chunks
+    subset = [0, 7, 19]
+    ref_o, ref_l = oracle_decode(w.meta, t.pool, t.q, batch=subset)
+    assert max_err(out, ref_o, rows=subset) <= TOL_BF16
+    assert lse_err(lse, ref_l, rows=subset) <= TOL_LSE
+    ws = workspace(gpu)
+    dw = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    dw.plan(t.kv_indptr, t.kv_indices, t.kv_last_page_len, w.hq, w.hkv, w.d, 16,
+            q_data_type=t.q.dtype, split_pages=0)
+    o_auto, l_auto = dw.run(t.q, t.pool, return_lse=True)
+    assert float((o_auto.float() - out.float()).abs().max()) <= 1e-2
+    assert float((l_auto - lse).abs().max()) <= 1e-3
+
+
+@pytest.mark.parametrize("d,hq,hkv", [(128, 64, 8), (64, 32, 4)])
+def test_decode_e4m3(gpu, d, hq, hkv):
+    meta, pool16, q = decode_case(gpu, EDGE_LENS, hq, hkv, d, seed=21)
+    pool8, scales = pagedattn.quantize_pages_e4m3(pool16)
+    ref_o, ref_l = oracle_decode(meta, pool8, q, scales=scales)
+    for split in (-1, 0, 8):
+        out, lse = run_decode(gpu, meta, pool8, q, hq, hkv, d, split_pages=split,
+                              kv_scales=scales)
+        assert max_err(out, ref_o) <= TOL_FP8, split
+        assert lse_err(lse, ref_l) <= TOL_LSE
