@@ -183,7 +183,7 @@ __device__ __forceinline__ void load_pair(Stage<D, BF16, FP8>& st,
     const int pg = pg0 + pi;
     int ntok = 0;
     int page = 0;
-    if (pg < page_hi && ind_lo + pg < p.num_indices) {
+    if (pg < page_hi && ind_lo >= 0 && ind_lo + pg < p.num_indices) {
       page = uniform(p.kv_indices[ind_lo + pg]);
       if (page >= 0 && page < p.num_pages) ntok = (pg == npages - 1) ? last : kPage;
       else page = 0;
