@@ -87,12 +87,9 @@ __device__ __forceinline__ uint16_t f2h(float f) {
   }
 }
 
-// fp8 e4m3fn (OCP, the gfx950 fp8 format) <-> fp32 through the hardware
-// converters.  Packing saturates nothing by itself: callers clamp to +-448.
-template <bool HI>
-__device__ __forceinline__ f32x2 e4m3x2_to_f32(uint32_t packed) {
-  return __builtin_amdgcn_cvt_pk_f32_fp8((int)packed, HI);
-}
+// fp32 -> fp8 e4m3fn (OCP, the gfx950 fp8 format) through the hardware
+// converter, round to nearest even.  It saturates nothing by itself: callers
+// clamp to +-448 first.
 __device__ __forceinline__ uint32_t f32_to_e4m3x4(float a, float b, float c,
                                                   float d) {
   int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);

@@ -91,46 +91,38 @@ __device__ __forceinline__ uint32_t dword_of(const T& v, int i) {
   }
 }
 
+// e4m3 -> 16-bit conversions through gfx950's scaled converters with a
+// unit scale: every e4m3 value is exact in bf16 and fp16.  (Extracting the
+// halves of v_cvt_pk_f32_fp8's fp32 pair instead is folded incorrectly by
+// this compiler: element 1 is replaced by element 0.)
+template <bool BF16, bool HI>
+__device__ __forceinline__ uint32_t e4m3x2_to_16(uint32_t w) {
+  if constexpr (BF16) {
+    return __builtin_bit_cast(
+        uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+  } else {
+    return __builtin_bit_cast(
+        uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+  }
+}
+
 // 8 e4m3 bytes -> 8 sixteen-bit values (bf16 or fp16), exact.
 template <bool BF16>
 __device__ __forceinline__ u32x4 e4m3x8_to_16(uint32_t lo, uint32_t hi) {
-  f32x2 f[4];
-  f[0] = e4m3x2_to_f32<false>(lo);
-  f[1] = e4m3x2_to_f32<true>(lo);
-  f[2] = e4m3x2_to_f32<false>(hi);
-  f[3] = e4m3x2_to_f32<true>(hi);
   u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if constexpr (BF16) {
-      // values of e4m3 are exact in bf16: keep the high half of the fp32
-      r[i] = (__builtin_bit_cast(uint32_t, f[i][0]) >> 16) |
-             (__builtin_bit_cast(uint32_t, f[i][1]) & 0xffff0000u);
-    } else {
-      r[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[i][0]) |
-             ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[i][1]) << 16);
-    }
-  }
+  r[0] = e4m3x2_to_16<BF16, false>(lo);
+  r[1] = e4m3x2_to_16<BF16, true>(lo);
+  r[2] = e4m3x2_to_16<BF16, false>(hi);
+  r[3] = e4m3x2_to_16<BF16, true>(hi);
   return r;
 }
 
 // 4 e4m3 bytes -> 4 sixteen-bit values.
 template <bool BF16>
 __device__ __forceinline__ u32x2 e4m3x4_to_16(uint32_t w) {
-  f32x2 f0 = e4m3x2_to_f32<false>(w);
-  f32x2 f1 = e4m3x2_to_f32<true>(w);
   u32x2 r;
-  if constexpr (BF16) {
-    r[0] = (__builtin_bit_cast(uint32_t, f0[0]) >> 16) |
-           (__builtin_bit_cast(uint32_t, f0[1]) & 0xffff0000u);
-    r[1] = (__builtin_bit_cast(uint32_t, f1[0]) >> 16) |
-           (__builtin_bit_cast(uint32_t, f1[1]) & 0xffff0000u);
-  } else {
-    r[0] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f0[0]) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f0[1]) << 16);
-    r[1] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f1[0]) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f1[1]) << 16);
-  }
+  r[0] = e4m3x2_to_16<BF16, false>(w);
+  r[1] = e4m3x2_to_16<BF16, true>(w);
   return r;
 }
 
