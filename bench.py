@@ -127,6 +127,64 @@ def bench_decode(w, args, dev, dtype, label, cpu_sample: int = 0):
     return res
 
 
+def bench_prefill(w, args, dev, dtype, label):
+    import numpy as np
+    import torch
+
+    import pagedattn
+    from pagedattn import workloads as W
+
+    flops = W.prefill_flops(w)
+    t = W.materialize(w, dev, dtype)
+    if w.fp8:
+        t.pool, t.scales = pagedattn.quantize_pages_e4m3(t.pool)
+    ws = torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
+    pw = pagedattn.BatchPrefillWithPagedKVCacheWrapper(ws, "HND")
+    pw.plan(t.qo_indptr, t.kv_indptr, t.kv_indices, t.kv_last_page_len, w.hq, w.hkv, w.d, 16,
+            q_data_type=dtype, causal=True)
+    out = torch.empty_like(t.q)
+
+    def step(ev=None):
+        pagedattn.append_paged_kv_cache(t.k_new, t.v_new, t.batch_indices, t.positions, t.pool,
+                                        t.kv_indices, t.kv_indptr, t.kv_last_page_len,
+                                        kv_layout="HND", kv_scales=t.scales)
+        if ev is not None:
+            ev[0].record()
+        pw.run(t.q, t.pool, kv_scales=t.scales, out=out)
+        if ev is not None:
+            ev[1].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        step(evs[i])
+    end.record()
+    torch.cuda.synchronize()
+    total_ms = start.elapsed_time(end)
+    attn = [a.elapsed_time(b) for a, b in evs]
+    avg = sum(attn) / len(attn)
+    res = {
+        "workload": label,
+        "ms_per_step": total_ms / args.steps,
+        "attn_ms_avg": avg,
+        "attn_ms_median": float(np.median(attn)),
+        "attn_TFLOPs": flops / (avg * 1e-3) / 1e12,
+        "alg_flops_attn": flops,
+        "rows": int(w.meta.nnz),
+        "kv_tokens": int(w.meta.seq_lens.sum()),
+    }
+    res["attn_frac"] = res["attn_TFLOPs"] / BF16_PEAK_TFLOPS
+    del t, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_decode_baseline(w, t, n_seq: int, kv_elem: int):
     """fp32 oracle decode over the first n_seq sequences, timed on the host."""
     import numpy as np
@@ -234,6 +292,23 @@ def main() -> int:
         extra["llama3_8b_long_decode"] = {k: lr[k] for k in (
             "ms_per_step", "attn_ms_avg", "attn_GBps", "attn_frac", "alg_bytes_attn",
             "split_pages", "batch", "kv_tokens")}
+        pa_ = argparse.Namespace(steps=max(5, args.steps // 2), warmup=2)
+        pr = bench_prefill(W.llama3_8b_prefill(seed=args.seed), pa_, dev, dtype,
+                           "llama3_8b_prefill")
+        log(f"llama3_8b_prefill: attention {pr['attn_ms_avg']:.4f} ms = "
+            f"{pr['attn_TFLOPs']:.1f} TFLOP/s ({100 * pr['attn_frac']:.1f}% of bf16 peak)")
+        extra["llama3_8b_prefill"] = pr
+        dec5, pre5 = W.llama3_70b_mixed_fp8(seed=args.seed)
+        d5 = bench_decode(dec5, pa_, dev, dtype, "llama3_70b_mixed_fp8.decode")
+        p5 = bench_prefill(pre5, pa_, dev, dtype, "llama3_70b_mixed_fp8.prefill")
+        log(f"llama3_70b_mixed_fp8: decode {d5['attn_GBps']:.0f} GB/s "
+            f"({100 * d5['attn_frac']:.1f}%), prefill {p5['attn_TFLOPs']:.1f} TFLOP/s "
+            f"({100 * p5['attn_frac']:.1f}% of bf16 peak)")
+        extra["llama3_70b_mixed_fp8"] = {
+            "decode": {k: d5[k] for k in ("attn_ms_avg", "attn_GBps", "attn_frac",
+                                          "alg_bytes_attn", "batch", "kv_tokens")},
+            "prefill": p5,
+        }
     cal = copy_calibration(dev)
     log(f"copy calibration: {cal['GBps']:.0f} GB/s (read+write)")
 

@@ -1,12 +1,544 @@
-// placeholder until the MFMA prefill kernel lands
+// Ragged, paged, causal prefill attention for gfx950
+// (BatchPrefillWithPagedKVCacheWrapper, src/models/llama.py:86-116 plan and
+// :212-228 run).
+//
+// Work unit: a tile of ROWS query rows of one sequence and one KV head, where
+// a row is (query token, query head of the group): rows are token-major with
+// the g = Hq/Hkv heads of a token adjacent, so every K/V tile staged in LDS
+// serves all heads of the group.  A 256-thread workgroup runs 4 waves; wave w
+// owns RB blocks of 32 rows.  The KV loop walks 64-token tiles (4 pages):
+//
+//   S^T[64 tok x 32 rows] = K[tok x D] . Q^T          v_mfma_f32_32x32x16_bf16
+//   O^T[D x 32 rows]     += V^T[D x 64 tok] . P^T      (P stays in registers)
+//
+// The S^T accumulator layout (lane = row, 16 registers = tokens) is already
+// the B-operand layout that PV needs once the token order inside each
+// 16-token step is permuted the same way on both operands, so P never leaves
+// registers; a lane's row max / sum need one cross-half exchange.  K and V
+// tiles are staged row-major in LDS (coalesced 16-byte loads, 16-byte LDS
+// writes); the V^T operand is read with ds_read_b64_tr_b16, whose 16-lane
+// groups return the transposed 4x16 block, so no transposing writes exist.
+// Loads use buffer resources sized to each page's valid tokens: absent pages
+// and slots past last_page_len read as zero without touching memory.
+// Causal tiles entirely below the diagonal skip masking; tiles above the last
+// row's diagonal are never visited.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <type_traits>
+#include <vector>
+
 #include "plan_internal.h"
+
+namespace pa {
+
+struct PrefillParams {
+  const PrefillItem* items;
+  const uint16_t* q;
+  int64_t q_sn, q_sh;
+  const int32_t* qo_indptr;
+  const uint8_t* cache;
+  const float* kv_scales;
+  int32_t num_pages;
+  const int32_t* kv_indices;
+  int32_t num_indices;
+  const int32_t* kv_indptr;
+  const int32_t* last_page_len;
+  uint16_t* out;  // [nnz, hq, D]
+  float* lse;     // [nnz, hq] or null
+  int32_t hq, hkv, g, causal;
+  float scale_log2;
+};
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+template <bool BF16>
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+        0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(
+        __builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+template <bool BF16, bool HI>
+__device__ __forceinline__ uint32_t e4m3x2_to16(uint32_t w) {
+  if constexpr (BF16) {
+    return __builtin_bit_cast(
+        uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI));
+  } else {
+    return __builtin_bit_cast(
+        uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI));
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ uint32_t pack2h(float a, float b) {
+  return (uint32_t)f2h<BF16>(a) | ((uint32_t)f2h<BF16>(b) << 16);
+}
+
+template <int D, bool BF16, bool FP8, int RB>
+struct PrefillCfg {
+  static constexpr int ESZ = FP8 ? 1 : 2;
+  static constexpr int BN = 64;             // kv tokens per tile
+  static constexpr int ROWS = 4 * 32 * RB;  // rows per workgroup
+  static constexpr int KS = D / 16;         // QK k-steps
+  static constexpr int DT = D / 32;         // PV d tiles
+  // LDS row strides (elements): K rows read 16 B per lane at one column
+  // (conflict-free for 16 consecutive rows when the stride is 4 mod 64
+  // dwords); V rows are read 4 at a time by the transpose read (disjoint
+  // 8-dword bank ranges when the stride is 8 mod 64 dwords).
+  static constexpr int KSTR = D + 8;
+  static constexpr int VSTR = D + 16;
+  static constexpr int CHUNKS = BN * D / 8;   // 16-byte (bf16) chunks per tile
+  static constexpr int CPT = CHUNKS / 256;    // chunks per thread
+  static constexpr int PAGE_BYTES = kPage * D * ESZ;
+  using Raw = typename std::conditional<FP8, u32x2, u32x4>::type;
+};
+
+template <int D, bool BF16, bool FP8, int RB>
+struct TileRegs {
+  using C = PrefillCfg<D, BF16, FP8, RB>;
+  typename C::Raw k[C::CPT];
+  typename C::Raw v[C::CPT];
+};
+
+// Issue the global loads of K/V tile `tile` (always the same number of loads:
+// missing pages are zero-sized buffers).
+template <int D, bool BF16, bool FP8, int RB>
+__device__ __forceinline__ void load_tile(TileRegs<D, BF16, FP8, RB>& tr,
+                                          const PrefillParams& p, int h,
+                                          int ind_lo, int npages, int last,
+                                          int tile) {
+  using C = PrefillCfg<D, BF16, FP8, RB>;
+#pragma unroll
+  for (int k = 0; k < C::CPT; ++k) {
+    const int c = threadIdx.x + 256 * k;
+    const int tok = c / (D / 8);
+    const int d0 = (c % (D / 8)) * 8;
+    // the 64 chunks of a wave lie in one page
+    const int pg = uniform(tile * 4 + tok / kPage);
+    int ntok = 0, page = 0;
+    if (pg < npages && ind_lo >= 0 && ind_lo + pg < p.num_indices) {
+      page = uniform(p.kv_indices[ind_lo + pg]);
+      if (page >= 0 && page < p.num_pages)
+        ntok = pg == npages - 1 ? last : kPage;
+      else
+        page = 0;
+    }
+    const uint8_t* kb =
+        p.cache + ((int64_t)page * 2 * p.hkv + h) * (int64_t)C::PAGE_BYTES;
+    const uint8_t* vb = kb + (int64_t)p.hkv * C::PAGE_BYTES;
+    const uint32_t bytes = (uint32_t)(ntok * D * C::ESZ);
+    const uint32_t off = (uint32_t)(((tok % kPage) * D + d0) * C::ESZ);
+    if constexpr (FP8) {
+      tr.k[k] = buf_load8(make_rsrc(kb, bytes), off);
+      tr.v[k] = buf_load8(make_rsrc(vb, bytes), off);
+    } else {
+      tr.k[k] = buf_load16(make_rsrc(kb, bytes), off);
+      tr.v[k] = buf_load16(make_rsrc(vb, bytes), off);
+    }
+  }
+}
+
+template <int D, bool BF16, bool FP8, int RB>
+__device__ __forceinline__ void store_tile(const TileRegs<D, BF16, FP8, RB>& tr,
+                                           uint16_t* ks, uint16_t* vs) {
+  using C = PrefillCfg<D, BF16, FP8, RB>;
+#pragma unroll
+  for (int k = 0; k < C::CPT; ++k) {
+    const int c = threadIdx.x + 256 * k;
+    const int tok = c / (D / 8);
+    const int d0 = (c % (D / 8)) * 8;
+    u32x4 kx, vx;
+    if constexpr (FP8) {
+      kx[0] = e4m3x2_to16<BF16, false>(tr.k[k][0]);
+      kx[1] = e4m3x2_to16<BF16, true>(tr.k[k][0]);
+      kx[2] = e4m3x2_to16<BF16, false>(tr.k[k][1]);
+      kx[3] = e4m3x2_to16<BF16, true>(tr.k[k][1]);
+      vx[0] = e4m3x2_to16<BF16, false>(tr.v[k][0]);
+      vx[1] = e4m3x2_to16<BF16, true>(tr.v[k][0]);
+      vx[2] = e4m3x2_to16<BF16, false>(tr.v[k][1]);
+      vx[3] = e4m3x2_to16<BF16, true>(tr.v[k][1]);
+    } else {
+      kx = tr.k[k];
+      vx = tr.v[k];
+    }
+    *reinterpret_cast<u32x4*>(ks + tok * C::KSTR + d0) = kx;
+    *reinterpret_cast<u32x4*>(vs + tok * C::VSTR + d0) = vx;
+  }
+}
+
+template <int D, bool BF16, bool FP8, int RB>
+__global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
+  using C = PrefillCfg<D, BF16, FP8, RB>;
+  constexpr int BN = C::BN;
+  __shared__ __attribute__((aligned(16))) uint16_t ks[BN * C::KSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[BN * C::VSTR];
+  __shared__ float kv_sc[2][4];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int col = lane & 31;   // row of the 32-row block this lane owns
+  const int half = lane >> 5;  // k-half of the MFMA operands
+  const int h = blockIdx.y;
+  const int g = p.g;
+
+  const PrefillItem item = p.items[blockIdx.x];
+  const int b = uniform(item.b);
+  const int qo_start = uniform(p.qo_indptr[b]);
+  const int qo_len = max(0, uniform(p.qo_indptr[b + 1]) - qo_start);
+  const int q_lo = uniform(item.q_lo);
+  const int q_hi = min(uniform(item.q_hi), qo_len);
+  if (q_lo >= q_hi) return;
+  const int ind_lo = uniform(p.kv_indptr[b]);
+  const int npages = max(0, uniform(p.kv_indptr[b + 1]) - ind_lo);
+  const int last = min(max(uniform(p.last_page_len[b]), 1), kPage);
+  const int kv_len = npages > 0 ? (npages - 1) * kPage + last : 0;
+  const int diag = kv_len - qo_len;  // row i sees kv j <= diag + i
+  const int kv_end =
+      p.causal ? min(kv_len, max(0, diag + q_hi)) : kv_len;
+  const int clean_end =
+      p.causal ? min(kv_len, max(0, diag + q_lo + 1)) : kv_len;
+  const int n_tiles = (kv_end + BN - 1) / BN;
+
+  // ---- Q^T fragments (B operand): lane -> row, 8 consecutive d per k-step
+  u32x4 qf[RB][C::KS];
+  int lim[RB];       // last visible kv index of the lane's row
+  bool rvalid[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int row = 32 * (RB * wave + rb) + col;
+    const int qi = q_lo + row / g;
+    rvalid[rb] = qi < q_hi;
+    lim[rb] = p.causal ? diag + qi : kv_len - 1;
+    const uint16_t* qp =
+        p.q + (int64_t)(qo_start + (rvalid[rb] ? qi : q_lo)) * p.q_sn +
+        (int64_t)(h * g + row % g) * p.q_sh + 8 * half;
+#pragma unroll
+    for (int ks_ = 0; ks_ < C::KS; ++ks_) {
+      u32x4 z = {0u, 0u, 0u, 0u};
+      if (rvalid[rb]) z = *reinterpret_cast<const u32x4*>(qp + 16 * ks_);
+      qf[rb][ks_] = z;
+    }
+  }
+
+  f32x16 o[RB][C::DT];
+  float m[RB], l[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) o[rb][dt] = f32x16{};
+    m[rb] = -INFINITY;
+    l[rb] = 0.f;
+  }
+
+  TileRegs<D, BF16, FP8, RB> tr;
+  if (n_tiles > 0) load_tile(tr, p, h, ind_lo, npages, last, 0);
+
+  for (int t = 0; t < n_tiles; ++t) {
+    store_tile(tr, ks, vs);
+    if constexpr (FP8) {
+      if (threadIdx.x < 8) {
+        const int pg = t * 4 + (threadIdx.x & 3);
+        float sc = 0.f;
+        if (pg < npages && ind_lo + pg < p.num_indices) {
+          const int page = p.kv_indices[ind_lo + pg];
+          if (page >= 0 && page < p.num_pages)
+            sc = p.kv_scales[((int64_t)page * 2 + (threadIdx.x >> 2)) * p.hkv + h];
+        }
+        kv_sc[threadIdx.x >> 2][threadIdx.x & 3] = sc;
+      }
+    }
+    __syncthreads();
+    // next tile's loads stay in flight during this tile's math
+    if (t + 1 < n_tiles) load_tile(tr, p, h, ind_lo, npages, last, t + 1);
+
+    // ---- S^T = K . Q^T
+    f32x16 s[RB][2];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) s[rb][0] = s[rb][1] = f32x16{};
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int ks_ = 0; ks_ < C::KS; ++ks_) {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(
+            ks + (32 * mt + col) * C::KSTR + 16 * ks_ + 8 * half);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) s[rb][mt] = mfma32<BF16>(a, qf[rb][ks_], s[rb][mt]);
+      }
+    }
+
+    // ---- online softmax; lane holds 32 of the tile's 64 tokens of its row
+    const int tok0 = t * BN;
+    const bool need_mask = tok0 + BN > clean_end;
+    float ksc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ksc[i] = FP8 ? kv_sc[0][i] * p.scale_log2 : p.scale_log2;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          float v = s[rb][mt][i] * ksc[2 * mt + (i >> 3)];
+          if (need_mask) {
+            const int tok = tok0 + 32 * mt + 8 * (i >> 2) + 4 * half + (i & 3);
+            if (tok > lim[rb] || tok >= kv_len) v = -INFINITY;
+          }
+          s[rb][mt][i] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m[rb], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m[rb] - m_use);
+      float rs = 0.f;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float e = exp2f(s[rb][mt][i] - m_use);
+          s[rb][mt][i] = e;
+          rs += e;
+        }
+      }
+      l[rb] = l[rb] * alpha + rs;
+      m[rb] = m_new;
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) o[rb][dt] *= alpha;
+    }
+
+    // ---- O^T += V^T . P^T over 4 steps of 16 tokens
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      u32x4 pb[RB];
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) {
+        const float vsc = FP8 ? kv_sc[1][st] : 1.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r0 = 8 * (st & 1) + 2 * i;
+          pb[rb][i] = pack2h<BF16>(s[rb][st >> 1][r0] * vsc, s[rb][st >> 1][r0 + 1] * vsc);
+        }
+      }
+      // transpose reads: lane (group qg, index L) points at
+      // V[16 st + 4 half + L/4 (+8)][32 dt + 16 (qg & 1) + 4 (L & 3)]
+      const int L = lane & 15;
+      const int qg = lane >> 4;
+      const int vrow = 16 * st + 4 * half + (L >> 2);
+      const int vcol = 16 * (qg & 1) + 4 * (L & 3);
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) {
+        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(vs + vrow * C::VSTR + 32 * dt + vcol));
+        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_i16x4*)(vs + (vrow + 8) * C::VSTR + 32 * dt + vcol));
+        u32x4 a;
+        a[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
+        a[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
+        a[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
+        a[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) o[rb][dt] = mfma32<BF16>(a, pb[rb], o[rb][dt]);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: O^T / l, lane's row, 4 consecutive d per register quad
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const float l_tot = l[rb] + __shfl_xor(l[rb], 32);
+    if (!rvalid[rb]) continue;
+    const int row = 32 * (RB * wave + rb) + col;
+    const int qi = q_lo + row / g;
+    const int head = h * g + row % g;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    uint16_t* orow = p.out + ((int64_t)(qo_start + qi) * p.hq + head) * D;
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt) {
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        u32x2 w;
+        w[0] = pack2h<BF16>(o[rb][dt][4 * i4] * inv, o[rb][dt][4 * i4 + 1] * inv);
+        w[1] = pack2h<BF16>(o[rb][dt][4 * i4 + 2] * inv, o[rb][dt][4 * i4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * half) = w;
+      }
+    }
+    if (p.lse && half == 0)
+      p.lse[(int64_t)(qo_start + qi) * p.hq + head] =
+          l_tot > 0.f ? (m[rb] + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+  }
+}
+
+using PrefillFn = void (*)(PrefillParams);
+
+constexpr int kPrefillRB = 1;
+
+template <int D, bool BF16, bool FP8>
+PrefillFn prefill_fn() {
+  return prefill_kernel<D, BF16, FP8, kPrefillRB>;
+}
+
+static PrefillFn pick_prefill(int d, bool bf16, bool fp8) {
+  if (d == 64) {
+    if (bf16) return fp8 ? prefill_fn<64, true, true>() : prefill_fn<64, true, false>();
+    return fp8 ? prefill_fn<64, false, true>() : prefill_fn<64, false, false>();
+  }
+  if (bf16) return fp8 ? prefill_fn<128, true, true>() : prefill_fn<128, true, false>();
+  return fp8 ? prefill_fn<128, false, true>() : prefill_fn<128, false, false>();
+}
+
+constexpr int kPrefillRows = 4 * 32 * kPrefillRB;
+
+}  // namespace pa
+
 using namespace pa;
+
 extern "C" {
-int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t*, const int32_t*, const int32_t*, int32_t, int32_t, int32_t, int32_t, int32_t, void*, size_t, void*) {
-  if (plan) plan->mode = kPlanNone;
-  return set_error(PAGEDATTN_ERR_UNSUPPORTED, "prefill_plan: not built yet");
+
+int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
+                           const int32_t* kv_indptr_host,
+                           const int32_t* kv_last_page_len_host,
+                           int32_t batch_size, int32_t num_qo_heads,
+                           int32_t num_kv_heads, int32_t head_dim,
+                           int32_t page_size, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+  const char* who = "prefill_plan";
+  if (!plan) return set_error(PAGEDATTN_ERR_INVALID, "%s: null plan", who);
+  plan->mode = kPlanNone;
+  if (batch_size < 0)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: batch_size %d < 0", who,
+                     batch_size);
+  int rc = validate_heads(who, num_qo_heads, num_kv_heads, head_dim, page_size);
+  if (rc) return rc;
+  if (!workspace || ((uintptr_t)workspace & (kWsAlign - 1)))
+    return set_error(PAGEDATTN_ERR_INVALID,
+                     "%s: workspace must be a 256-byte aligned device buffer",
+                     who);
+  if (batch_size > 0 && !qo_indptr_host)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: null qo_indptr", who);
+  std::vector<int32_t> npages, kv_len;
+  rc = validate_paged_metadata(who, kv_indptr_host, kv_last_page_len_host,
+                               batch_size, page_size, &npages, &kv_len);
+  if (rc) return rc;
+  if (batch_size > 0 && qo_indptr_host[0] < 0)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: qo_indptr[0] < 0", who);
+  const int g = num_qo_heads / num_kv_heads;
+  const int q_tile = kPrefillRows / g;
+  std::vector<PrefillItem> items;
+  std::vector<int64_t> cost;
+  for (int b = 0; b < batch_size; ++b) {
+    const int qo = qo_indptr_host[b + 1] - qo_indptr_host[b];
+    if (qo < 0)
+      return set_error(PAGEDATTN_ERR_INVALID,
+                       "%s: qo_indptr is not monotone at %d", who, b);
+    for (int lo = 0; lo < qo; lo += q_tile) {
+      const int hi = std::min(qo, lo + q_tile);
+      items.push_back(PrefillItem{b, lo, hi, -1});
+      // kv tokens the tile's last row can see (causal)
+      cost.push_back(std::max<int64_t>(
+          0, std::min<int64_t>(kv_len[b], (int64_t)kv_len[b] - qo + hi)));
+    }
+  }
+  // most expensive tiles first
+  std::vector<int> order(items.size());
+  for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
+  std::stable_sort(order.begin(), order.end(),
+                   [&](int a, int c) { return cost[a] > cost[c]; });
+  const size_t host_bytes = sizeof(PrefillItem) * items.size();
+  plan->host.assign((host_bytes + 3) / 4, 0);
+  auto* dst = reinterpret_cast<PrefillItem*>(plan->host.data());
+  for (size_t i = 0; i < order.size(); ++i) dst[i] = items[order[i]];
+  plan->workspace = workspace;
+  plan->workspace_bytes = workspace_bytes;
+  rc = upload_plan(plan, who, host_bytes, ws_align(kWsHeader + host_bytes),
+                   stream);
+  if (rc) return rc;
+  plan->batch_size = batch_size;
+  plan->hq = num_qo_heads;
+  plan->hkv = num_kv_heads;
+  plan->d = head_dim;
+  plan->page_size = page_size;
+  plan->n_items = (int)items.size();
+  plan->n_merge = 0;
+  plan->n_slots = 0;
+  plan->q_tile = q_tile;
+  plan->total_qo =
+      batch_size > 0 ? (int64_t)qo_indptr_host[batch_size] - qo_indptr_host[0] : 0;
+  plan->items_dev = static_cast<char*>(workspace) + kWsHeader;
+  plan->mode = kPlanPrefill;
+  return PAGEDATTN_OK;
 }
-int pagedattn_prefill_run(const pagedattn_plan*, const void*, int64_t, int64_t, int32_t, const int32_t*, const void*, int32_t, const float*, int32_t, const int32_t*, int32_t, const int32_t*, const int32_t*, void*, float*, int32_t, float, void*) {
-  return set_error(PAGEDATTN_ERR_UNSUPPORTED, "prefill_run: not built yet");
+
+int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
+                          int64_t q_stride_n, int64_t q_stride_h,
+                          int32_t q_dtype, const int32_t* qo_indptr,
+                          const void* paged_kv_cache, int32_t kv_dtype,
+                          const float* kv_scales, int32_t num_pages,
+                          const int32_t* kv_indices, int32_t num_indices,
+                          const int32_t* kv_indptr,
+                          const int32_t* kv_last_page_len, void* out,
+                          float* lse, int32_t causal, float sm_scale,
+                          void* stream) {
+  const char* who = "prefill_run";
+  if (!plan || plan->mode != kPlanPrefill)
+    return set_error(PAGEDATTN_ERR_PLAN,
+                     "%s: no prefill plan (call plan first)", who);
+  if (q_dtype != PAGEDATTN_BF16 && q_dtype != PAGEDATTN_F16)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: q dtype %d not supported",
+                     who, q_dtype);
+  const bool fp8 = kv_dtype == PAGEDATTN_E4M3;
+  if (!fp8 && kv_dtype != q_dtype)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                     "%s: kv dtype %d must equal q dtype %d or be e4m3", who,
+                     kv_dtype, q_dtype);
+  if (fp8 && !kv_scales)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: e4m3 pool needs kv_scales",
+                     who);
+  if (plan->n_items == 0) return PAGEDATTN_OK;
+  if (!q || !qo_indptr || !paged_kv_cache || !kv_indices || !kv_indptr ||
+      !kv_last_page_len || !out)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: null pointer", who);
+  if ((q_stride_n & 7) || (q_stride_h & 7) || !aligned16(q) ||
+      !aligned16(paged_kv_cache) || !aligned16(out))
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                     "%s: q, out and the pool must be 16-byte aligned with "
+                     "strides that are multiples of 8 elements",
+                     who);
+  if (num_pages < 0 || num_indices < 0)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: negative sizes", who);
+  PrefillParams p;
+  p.items = static_cast<const PrefillItem*>(plan->items_dev);
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_sn = q_stride_n;
+  p.q_sh = q_stride_h;
+  p.qo_indptr = qo_indptr;
+  p.cache = static_cast<const uint8_t*>(paged_kv_cache);
+  p.kv_scales = kv_scales;
+  p.num_pages = num_pages;
+  p.kv_indices = kv_indices;
+  p.num_indices = num_indices;
+  p.kv_indptr = kv_indptr;
+  p.last_page_len = kv_last_page_len;
+  p.out = static_cast<uint16_t*>(out);
+  p.lse = lse;
+  p.hq = plan->hq;
+  p.hkv = plan->hkv;
+  p.g = plan->hq / plan->hkv;
+  p.causal = causal ? 1 : 0;
+  p.scale_log2 = sm_scale * 1.4426950408889634f;
+  PrefillFn fn = pick_prefill(plan->d, q_dtype == PAGEDATTN_BF16, fp8);
+  hipLaunchKernelGGL(fn, dim3(plan->n_items, plan->hkv), dim3(256), 0,
+                     (hipStream_t)stream, p);
+  return check_launch(who);
 }
-}
+
+}  // extern "C"

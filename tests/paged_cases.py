@@ -111,3 +111,56 @@ def lse_err(lse, ref, rows=None):
     fin = torch.isfinite(ref)
     assert torch.equal(torch.isfinite(a), fin), "lse -inf pattern differs"
     return float((a[fin] - ref[fin]).abs().max()) if fin.any() else 0.0
+
+
+def prefill_case(device, computed, chunks, hq, hkv, d, dtype=torch.bfloat16, seed=0):
+    rng = np.random.default_rng(seed)
+    lens = [c + n for c, n in zip(computed, chunks)]
+    tables, num_pages = random_tables(rng, lens)
+    meta = prefill_metadata(tables, computed, chunks)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    pool = torch.randn((num_pages, 2, hkv, 16, d), generator=g, device=device,
+                       dtype=torch.float32).to(dtype)
+    q = strided_rows(meta.nnz, hq, d, dtype, device, g, lead=0, tail=2 * hkv)
+    return meta, pool, q
+
+
+def run_prefill(device, meta, pool, q, hq, hkv, d, causal=True, kv_scales=None, ws=None):
+    ws = workspace(device) if ws is None else ws
+    w = pagedattn.BatchPrefillWithPagedKVCacheWrapper(ws, "HND")
+    w.plan(i32(meta.qo_indptr, device), i32(meta.kv_indptr, device),
+           i32(meta.kv_indices, device), i32(meta.kv_last_page_len, device), hq, hkv, d, 16,
+           q_data_type=q.dtype)
+    out, lse = w.run(q, pool, kv_scales=kv_scales, return_lse=True, causal=causal)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+def oracle_prefill_rows(meta, pool, q, b, lo, hi, causal=True, scales=None):
+    """Oracle rows [lo, hi) of sequence b's chunk: a causal row slice is a
+    bottom-right aligned chunk over the first kv - qo + hi keys."""
+    indptr, ind, last, sub, sub_scales = compact(meta, pool, [b], scales)
+    k, v = O.gather_pages(sub, indptr, ind, last, 0, sub_scales)
+    qo = int(meta.qo_indptr[b + 1] - meta.qo_indptr[b])
+    kv = k.shape[0]
+    q0 = int(meta.qo_indptr[b])
+    if causal:
+        n_keys = max(0, kv - qo + hi)
+        return O.attention(q[q0 + lo:q0 + hi].float().cpu(), k[:n_keys], v[:n_keys], causal=True)
+    return O.attention(q[q0 + lo:q0 + hi].float().cpu(), k, v, causal=False)
+
+
+def oracle_prefill(meta, pool, q, causal=True, scales=None, row_block=256):
+    n = meta.nnz
+    out = torch.full((n,) + tuple(q.shape[1:]), float("nan"))
+    lse = torch.full((n, q.shape[1]), float("nan"))
+    for b in range(len(meta.kv_last_page_len)):
+        qo = int(meta.qo_indptr[b + 1] - meta.qo_indptr[b])
+        q0 = int(meta.qo_indptr[b])
+        for lo in range(0, qo, row_block):
+            hi = min(qo, lo + row_block)
+            o, l = oracle_prefill_rows(meta, pool, q, b, lo, hi, causal, scales)
+            out[q0 + lo:q0 + hi] = o
+            lse[q0 + lo:q0 + hi] = l
+    return out, lse
