@@ -206,12 +206,14 @@ def cpu_decode_baseline(w, t, n_seq: int, kv_elem: int):
     q = t.q[rows].float().cpu()
     ind = np.arange(len(pages), dtype=np.int32)
     last = m.kv_last_page_len[rows]
-    times = []
-    for _ in range(3):
+    # repeat the sample until about 10 s of CPU work has been timed
+    reps, elapsed = 0, 0.0
+    while elapsed < 10.0 or reps < 3:
         t0 = time.perf_counter()
         O.decode(q, sub, indptr, ind, last, scales=scales)
-        times.append(time.perf_counter() - t0)
-    sec = float(np.median(times))
+        elapsed += time.perf_counter() - t0
+        reps += 1
+    sec = elapsed / reps
     kv_bytes = int(m.seq_lens[rows].astype(np.int64).sum()) * w.hkv * w.d * 2 * kv_elem
     byts = kv_bytes + len(rows) * w.hq * w.d * 4
     try:
@@ -227,7 +229,7 @@ def cpu_decode_baseline(w, t, n_seq: int, kv_elem: int):
         "kind": "port",
         "sample": (f"{len(rows)} of {w.meta.batch_size} sequences of {w.name} "
                    f"({int(m.seq_lens[rows].sum())} kv tokens), fp32 torch oracle, "
-                   f"median of 3 = {sec:.3f} s on {model}"),
+                   f"{reps} passes in {elapsed:.1f} s ({sec:.3f} s each) on {model}"),
     }
 
 
@@ -278,7 +280,7 @@ def main() -> int:
 
     main_w = W.tinyllama_decode(seed=args.seed)
     r = bench_decode(main_w, args, dev, dtype, "tinyllama_decode",
-                     cpu_sample=0 if args.no_cpu else 64)
+                     cpu_sample=0 if args.no_cpu else 256)
     log(f"tinyllama_decode: step {r['ms_per_step']:.4f} ms, attention {r['attn_ms_avg']:.4f} ms "
         f"= {r['attn_GBps']:.0f} GB/s ({100 * r['attn_frac']:.1f}% of 8 TB/s)")
     extra = {}
