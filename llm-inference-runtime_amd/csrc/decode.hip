@@ -318,7 +318,9 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
   __shared__ float sm_l[4][16];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform by construction; readfirstlane tells the compiler, so page
+  // indices are scalar loads and buffer descriptors stay in SGPRs
+  const int wave = uniform(threadIdx.x >> 6);
   const int n = lane & 15;
   const int G = lane >> 4;
   const int h = blockIdx.y;

@@ -182,7 +182,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
   __shared__ float kv_sc[2][4];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = uniform(threadIdx.x >> 6);
   const int col = lane & 31;   // row of the 32-row block this lane owns
   const int half = lane >> 5;  // k-half of the MFMA operands
   const int h = blockIdx.y;
