@@ -143,6 +143,9 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return (uint32_t)f2h<BF16>(a) | ((uint32_t)f2h<BF16>(b) << 16);
 }
 
+// pages whose ids are staged in LDS at a time
+constexpr int kSegPages = 1024;
+
 template <int D, bool BF16, bool FP8>
 struct DecodeTraits {
   static constexpr int ESZ = FP8 ? 1 : 2;
@@ -164,22 +167,22 @@ struct Stage {
   float kscale[2], vscale[2];
 };
 
+// Page ids of the current segment live in LDS (staged once per segment), so
+// issuing a pair's loads costs one LDS read instead of a dependent HBM round
+// trip for the page id.  sm_pages[i] < 0 marks an absent or invalid page.
 template <int D, bool BF16, bool FP8>
 __device__ __forceinline__ void load_pair(Stage<D, BF16, FP8>& st,
                                           const DecodeParams& p, int h,
-                                          int ind_lo, int npages, int last,
-                                          int page_hi, int pg0, int n, int G) {
+                                          const int* sm_pages, int seg_lo,
+                                          int seg_hi, int npages, int last,
+                                          int pg0, int n, int G) {
   using Tr = DecodeTraits<D, BF16, FP8>;
 #pragma unroll
   for (int pi = 0; pi < 2; ++pi) {
     const int pg = pg0 + pi;
-    int ntok = 0;
-    int page = 0;
-    if (pg < page_hi && ind_lo >= 0 && ind_lo + pg < p.num_indices) {
-      page = uniform(p.kv_indices[ind_lo + pg]);
-      if (page >= 0 && page < p.num_pages) ntok = (pg == npages - 1) ? last : kPage;
-      else page = 0;
-    }
+    int page = pg < seg_hi ? uniform(sm_pages[pg - seg_lo]) : -1;
+    const int ntok = page < 0 ? 0 : (pg == npages - 1 ? last : kPage);
+    page = page < 0 ? 0 : page;
     st.ntok[pi] = ntok;
     const uint8_t* kbase =
         p.cache + ((int64_t)page * 2 * p.hkv + h) * (int64_t)Tr::PAGE_BYTES;
@@ -316,6 +319,7 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
   __shared__ float sm_o[4][16][OPAD];
   __shared__ float sm_m[4][16];
   __shared__ float sm_l[4][16];
+  __shared__ int sm_pages[kSegPages];
 
   const int lane = threadIdx.x & 63;
   // wave-uniform by construction; readfirstlane tells the compiler, so page
@@ -358,21 +362,34 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
     sm.m = -INFINITY;
     sm.l = 0.f;
 
-    const int n_pairs = page_hi > page_lo ? (page_hi - page_lo + 1) >> 1 : 0;
-    const int n_my = n_pairs > wave ? (n_pairs - wave + 3) >> 2 : 0;
-    if (n_my > 0) {
-      Stage<D, BF16, FP8> sa, sb;
-      load_pair(sa, p, h, ind_lo, npages, last, page_hi,
-                page_lo + 2 * wave, n, G);
-      for (int i = 0; i < n_my; i += 2) {
-        load_pair(sb, p, h, ind_lo, npages, last, page_hi,
-                  page_lo + 2 * (wave + 4 * (i + 1)), n, G);
-        compute_pair(sa, qf, sm, p.scale_log2, G);
-        if (i + 1 >= n_my) break;
-        load_pair(sa, p, h, ind_lo, npages, last, page_hi,
-                  page_lo + 2 * (wave + 4 * (i + 2)), n, G);
-        compute_pair(sb, qf, sm, p.scale_log2, G);
+    // segments of at most kSegPages pages: stage their page ids in LDS, then
+    // wave w takes page pairs w, w+4, ... of the segment
+    for (int seg_lo = page_lo; seg_lo < page_hi; seg_lo += kSegPages) {
+      const int seg_hi = min(page_hi, seg_lo + kSegPages);
+      for (int t = threadIdx.x; t < seg_hi - seg_lo; t += 256) {
+        const int idx = ind_lo + seg_lo + t;
+        int page = -1;
+        if (ind_lo >= 0 && idx < p.num_indices) page = p.kv_indices[idx];
+        sm_pages[t] = (page >= 0 && page < p.num_pages) ? page : -1;
       }
+      __syncthreads();
+      const int n_pairs = (seg_hi - seg_lo + 1) >> 1;
+      const int n_my = n_pairs > wave ? (n_pairs - wave + 3) >> 2 : 0;
+      if (n_my > 0) {
+        Stage<D, BF16, FP8> sa, sb;
+        load_pair(sa, p, h, sm_pages, seg_lo, seg_hi, npages, last,
+                  seg_lo + 2 * wave, n, G);
+        for (int i = 0; i < n_my; i += 2) {
+          load_pair(sb, p, h, sm_pages, seg_lo, seg_hi, npages, last,
+                    seg_lo + 2 * (wave + 4 * (i + 1)), n, G);
+          compute_pair(sa, qf, sm, p.scale_log2, G);
+          if (i + 1 >= n_my) break;
+          load_pair(sa, p, h, sm_pages, seg_lo, seg_hi, npages, last,
+                    seg_lo + 2 * (wave + 4 * (i + 2)), n, G);
+          compute_pair(sb, qf, sm, p.scale_log2, G);
+        }
+      }
+      __syncthreads();  // sm_pages is rewritten by the next segment
     }
     const float l_tot = sum_over_groups16(sm.l);
 
