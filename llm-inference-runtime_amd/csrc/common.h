@@ -67,6 +67,16 @@ __device__ __forceinline__ int uniform(int x) {
   return __builtin_amdgcn_readfirstlane(x);
 }
 
+// Load of data that no thread writes during the kernel (metadata, work
+// lists), through the constant address space: with a wave-uniform address
+// the compiler emits a scalar load instead of a vector load plus a wait on
+// every outstanding vector load.
+template <typename T>
+__device__ __forceinline__ T load_invariant(const T* ptr) {
+  using CT = const __attribute__((address_space(4))) T;
+  return *reinterpret_cast<CT*>(reinterpret_cast<uintptr_t>(ptr));
+}
+
 // 16-bit element helpers.  Storage is raw uint16 bits; IS_BF16 selects the
 // interpretation.
 template <bool IS_BF16>

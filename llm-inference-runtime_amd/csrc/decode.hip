@@ -1,13 +1,17 @@
 // Paged decode attention for gfx950 (BatchDecodeWithPagedKVCacheWrapper,
 // src/models/llama.py:119-147 plan and :230-245 run).
 //
-// Work unit: (page range of one sequence, one KV head) for all g = Hq/Hkv
-// query heads of that head's group, so each K/V byte is read from HBM once.
-// A 256-thread workgroup runs 4 waves; wave w takes page pairs w, w+4, ...
-// of its range and keeps its own online-softmax state, merged through LDS at
-// the end of the range.
+// Work unit: one wave owns a list of items; an item is (page range of one
+// sequence, one KV head) for all g = Hq/Hkv query heads of that head, so
+// each K/V byte is read from HBM once.  Waves are independent: no barriers,
+// no cross-wave LDS merges, so one slow memory request stalls one wave only.
+// The host planner cuts the concatenated (sequence, head, page) stream into
+// equal shares per wave; sequences cut at a share boundary write split
+// partials, and the last of a group's waves to finish merges them (an
+// arrival counter in the workspace, released/acquired with device-scope
+// fences), so one launch produces the final output.
 //
-// Per page pair (32 tokens) one wave does:
+// Per page pair (32 tokens) a wave does:
 //   S^T[32 tok x 16 heads] = K[tok x D] . Q^T      (v_mfma_f32_16x16x32, D/32 k-steps per page)
 //   O^T[D x 16 heads]     += V^T[D x 32 tok] . P^T (D/16 MFMAs, K = the 32 tokens)
 // Query heads occupy the MFMA N dimension (g <= 16, padded), tokens the
@@ -17,8 +21,9 @@
 // Loads go through buffer resources sized to the valid tokens of each page:
 // absent pages (num_records = 0) and slots past last_page_len read as zero
 // without touching HBM, so the loop issues a fixed number of loads per pair
-// and the compiler can keep the next pair's loads in flight while the
-// current one is computed (two register stages, ping-pong).
+// and the compiler keeps the next pair's loads in flight while the current
+// one is computed (two register stages, ping-pong).  Page ids are scalar
+// loads issued two pairs ahead of their use.
 //
 // K rows are read as 16-byte (bf16/fp16) or 8-byte (e4m3) pieces in the
 // MFMA A-operand layout (lane -> token row, 8 consecutive d).  V rows are
@@ -26,9 +31,11 @@
 // which gives W PV tiles whose row m is d = W m + e; the 8 tokens a lane
 // needs for one tile come from its own 8 loads, repacked with bit ops.
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <queue>
 #include <vector>
 
 #include "plan_internal.h"
@@ -37,7 +44,10 @@ namespace pa {
 
 struct DecodeParams {
   const DecodeItem* items;
-  const int32_t* wg_ptr;  // [gridDim.x + 1]: items of workgroup x
+  const int32_t* wave_ptr;  // [n_waves + 1]: items of wave w
+  const MergeItem* merges;
+  int32_t* counters;        // [n_merge] arrival counters (0 between launches)
+  int32_t n_waves, n_merge, n_slots, batch_size;
   const uint16_t* q;
   int64_t q_sn, q_sh;
   const uint8_t* cache;
@@ -49,8 +59,8 @@ struct DecodeParams {
   const int32_t* last_page_len;
   uint16_t* out;
   float* lse;
-  float* partial_o;
-  float* partial_lse;
+  float* partial_o;    // [n_slots, g, D]
+  float* partial_lse;  // [n_slots, g] (base 2)
   int32_t hq, hkv, g;
   float scale_log2;  // sm_scale * log2(e)
 };
@@ -143,9 +153,6 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   return (uint32_t)f2h<BF16>(a) | ((uint32_t)f2h<BF16>(b) << 16);
 }
 
-// pages whose ids are staged in LDS at a time
-constexpr int kSegPages = 1024;
-
 template <int D, bool BF16, bool FP8>
 struct DecodeTraits {
   static constexpr int ESZ = FP8 ? 1 : 2;
@@ -167,20 +174,36 @@ struct Stage {
   float kscale[2], vscale[2];
 };
 
-// Page ids of the current segment live in LDS (staged once per segment), so
-// issuing a pair's loads costs one LDS read instead of a dependent HBM round
-// trip for the page id.  sm_pages[i] < 0 marks an absent or invalid page.
+// Page ids of a pair, fetched with scalar loads two pairs ahead of use
+// (-1: absent or invalid page).
+struct PairIds {
+  int p0, p1;
+};
+
+__device__ __forceinline__ int page_id(const DecodeParams& p, int ind_lo,
+                                       int pg, int page_hi) {
+  int page = -1;
+  if (pg < page_hi && ind_lo >= 0 && ind_lo + pg < p.num_indices)
+    page = uniform(load_invariant(p.kv_indices + ind_lo + pg));
+  return (page >= 0 && page < p.num_pages) ? page : -1;
+}
+
+__device__ __forceinline__ PairIds fetch_ids(const DecodeParams& p, int ind_lo,
+                                             int pg0, int page_hi) {
+  return PairIds{page_id(p, ind_lo, pg0, page_hi),
+                 page_id(p, ind_lo, pg0 + 1, page_hi)};
+}
+
 template <int D, bool BF16, bool FP8>
 __device__ __forceinline__ void load_pair(Stage<D, BF16, FP8>& st,
                                           const DecodeParams& p, int h,
-                                          const int* sm_pages, int seg_lo,
-                                          int seg_hi, int npages, int last,
-                                          int pg0, int n, int G) {
+                                          PairIds ids, int pg0, int npages,
+                                          int last, int n, int G) {
   using Tr = DecodeTraits<D, BF16, FP8>;
 #pragma unroll
   for (int pi = 0; pi < 2; ++pi) {
     const int pg = pg0 + pi;
-    int page = pg < seg_hi ? uniform(sm_pages[pg - seg_lo]) : -1;
+    int page = pi ? ids.p1 : ids.p0;
     const int ntok = page < 0 ? 0 : (pg == npages - 1 ? last : kPage);
     page = page < 0 ? 0 : page;
     st.ntok[pi] = ntok;
@@ -200,8 +223,8 @@ __device__ __forceinline__ void load_pair(Stage<D, BF16, FP8>& st,
           rv, (uint32_t)(((4 * G + r) * D + Tr::W * n) * Tr::ESZ));
     if constexpr (FP8) {
       const int64_t si = ((int64_t)page * 2) * p.hkv + h;
-      st.kscale[pi] = ntok ? p.kv_scales[si] : 0.f;
-      st.vscale[pi] = ntok ? p.kv_scales[si + p.hkv] : 0.f;
+      st.kscale[pi] = ntok ? load_invariant(p.kv_scales + si) : 0.f;
+      st.vscale[pi] = ntok ? load_invariant(p.kv_scales + si + p.hkv) : 0.f;
     }
   }
 }
@@ -311,36 +334,69 @@ __device__ __forceinline__ void compute_pair(const Stage<D, BF16, FP8>& st,
   }
 }
 
+// Merge of one split group by the last wave to finish:
+// o = sum_c 2^(lse_c - M) o_c / sum_c 2^(lse_c - M), lse = M + log2(sum ...).
+template <int D, bool BF16>
+__device__ __forceinline__ void merge_group(const DecodeParams& p,
+                                            const MergeItem& mi, int lane) {
+  const int g = p.g;
+  for (int idx = lane; idx < g * D; idx += kWave) {
+    const int hn = idx / D;
+    const int dd = idx - hn * D;
+    float M = -INFINITY;
+    for (int s = 0; s < mi.nslots; ++s)
+      M = fmaxf(M, p.partial_lse[(int64_t)(mi.slot0 + s) * g + hn]);
+    float num = 0.f, den = 0.f;
+    if (M != -INFINITY) {
+      for (int s = 0; s < mi.nslots; ++s) {
+        const int64_t sh = (int64_t)(mi.slot0 + s) * g + hn;
+        const float wt = exp2f(p.partial_lse[sh] - M);
+        den += wt;
+        num += wt * p.partial_o[sh * D + dd];
+      }
+    }
+    const int head = mi.h * g + hn;
+    p.out[((int64_t)mi.b * p.hq + head) * D + dd] =
+        f2h<BF16>(M != -INFINITY ? num / den : 0.f);
+    if (p.lse && dd == 0)
+      p.lse[(int64_t)mi.b * p.hq + head] =
+          M != -INFINITY ? (M + log2f(den)) * 0.69314718055994531f : -INFINITY;
+  }
+}
+
 template <int D, bool BF16, bool FP8>
 __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
-  constexpr int OPAD = D + 4;
-  __shared__ float sm_o[4][16][OPAD];
-  __shared__ float sm_m[4][16];
-  __shared__ float sm_l[4][16];
-  __shared__ int sm_pages[kSegPages];
-
   const int lane = threadIdx.x & 63;
-  // wave-uniform by construction; readfirstlane tells the compiler, so page
-  // indices are scalar loads and buffer descriptors stay in SGPRs
+  // wave-uniform by construction; readfirstlane tells the compiler, so item
+  // fields are scalar loads and buffer descriptors stay in SGPRs
   const int wave = uniform(threadIdx.x >> 6);
+  const int gw = uniform((int)blockIdx.x * 4 + wave);
+  if (gw >= p.n_waves) return;
   const int n = lane & 15;
   const int G = lane >> 4;
-  const int h = blockIdx.y;
   const int g = p.g;
 
-  const int it_lo = p.wg_ptr[blockIdx.x];
-  const int it_hi = p.wg_ptr[blockIdx.x + 1];
+  const int it_lo = uniform(load_invariant(p.wave_ptr + gw));
+  const int it_hi = uniform(load_invariant(p.wave_ptr + gw + 1));
   for (int it = it_lo; it < it_hi; ++it) {
-    const DecodeItem item = p.items[it];
-    const int b = uniform(item.b);
-    const int ind_lo = uniform(p.kv_indptr[b]);
-    const int npages = max(0, uniform(p.kv_indptr[b + 1]) - ind_lo);
-    const int last = min(max(uniform(p.last_page_len[b]), 1), kPage);
-    const int page_lo = uniform(item.page_lo);
-    const int page_hi = min(uniform(item.page_hi), npages);
-    const int slot = uniform(item.slot);
+    const int32_t* itp = reinterpret_cast<const int32_t*>(p.items + it);
+    const int b = uniform(load_invariant(itp + 0));
+    const int h = uniform(load_invariant(itp + 1));
+    const int item_lo = uniform(load_invariant(itp + 2));
+    const int item_hi = uniform(load_invariant(itp + 3));
+    const int slot = uniform(load_invariant(itp + 4));
+    const int merge = uniform(load_invariant(itp + 5));
+    // a work list that does not match this launch is skipped, never followed
+    if (b < 0 || b >= p.batch_size || h < 0 || h >= p.hkv ||
+        slot >= p.n_slots || merge >= p.n_merge || (slot >= 0) != (merge >= 0))
+      continue;
+    const int ind_lo = uniform(load_invariant(p.kv_indptr + b));
+    const int npages = max(0, uniform(load_invariant(p.kv_indptr + b + 1)) - ind_lo);
+    const int last = min(max(uniform(load_invariant(p.last_page_len + b)), 1), kPage);
+    const int page_lo = max(0, item_lo);
+    const int page_hi = min(item_hi, npages);
 
     // Q fragments: lane (G, n) holds head n, d in [32 ks + 8 G, +8)
     u32x4 qf[D / 32];
@@ -362,107 +418,76 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
     sm.m = -INFINITY;
     sm.l = 0.f;
 
-    // segments of at most kSegPages pages: stage their page ids in LDS, then
-    // wave w takes page pairs w, w+4, ... of the segment
-    for (int seg_lo = page_lo; seg_lo < page_hi; seg_lo += kSegPages) {
-      const int seg_hi = min(page_hi, seg_lo + kSegPages);
-      for (int t = threadIdx.x; t < seg_hi - seg_lo; t += 256) {
-        const int idx = ind_lo + seg_lo + t;
-        int page = -1;
-        if (ind_lo >= 0 && idx < p.num_indices) page = p.kv_indices[idx];
-        sm_pages[t] = (page >= 0 && page < p.num_pages) ? page : -1;
+    // two register stages (ping-pong); page ids run two pairs ahead
+    const int n_pairs = page_hi > page_lo ? (page_hi - page_lo + 1) >> 1 : 0;
+    if (n_pairs > 0) {
+      Stage<D, BF16, FP8> sa, sb;
+      PairIds id_b = fetch_ids(p, ind_lo, page_lo + 2, page_hi);
+      load_pair(sa, p, h, fetch_ids(p, ind_lo, page_lo, page_hi), page_lo,
+                npages, last, n, G);
+      for (int i = 0; i < n_pairs; i += 2) {
+        const PairIds id_a = fetch_ids(p, ind_lo, page_lo + 2 * (i + 2), page_hi);
+        load_pair(sb, p, h, id_b, page_lo + 2 * (i + 1), npages, last, n, G);
+        compute_pair(sa, qf, sm, p.scale_log2, G);
+        if (i + 1 >= n_pairs) break;
+        id_b = fetch_ids(p, ind_lo, page_lo + 2 * (i + 3), page_hi);
+        load_pair(sa, p, h, id_a, page_lo + 2 * (i + 2), npages, last, n, G);
+        compute_pair(sb, qf, sm, p.scale_log2, G);
       }
-      __syncthreads();
-      const int n_pairs = (seg_hi - seg_lo + 1) >> 1;
-      const int n_my = n_pairs > wave ? (n_pairs - wave + 3) >> 2 : 0;
-      if (n_my > 0) {
-        Stage<D, BF16, FP8> sa, sb;
-        load_pair(sa, p, h, sm_pages, seg_lo, seg_hi, npages, last,
-                  seg_lo + 2 * wave, n, G);
-        for (int i = 0; i < n_my; i += 2) {
-          load_pair(sb, p, h, sm_pages, seg_lo, seg_hi, npages, last,
-                    seg_lo + 2 * (wave + 4 * (i + 1)), n, G);
-          compute_pair(sa, qf, sm, p.scale_log2, G);
-          if (i + 1 >= n_my) break;
-          load_pair(sa, p, h, sm_pages, seg_lo, seg_hi, npages, last,
-                    seg_lo + 2 * (wave + 4 * (i + 2)), n, G);
-          compute_pair(sb, qf, sm, p.scale_log2, G);
-        }
-      }
-      __syncthreads();  // sm_pages is rewritten by the next segment
     }
+
+    // ---- epilogue from registers: lane (G, n) owns d = W (4 G + r) + e of
+    // head n
     const float l_tot = sum_over_groups16(sm.l);
-
-    // ---- merge the four waves through LDS
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const float lse2 = l_tot > 0.f ? sm.m + log2f(l_tot) : -INFINITY;
+    if (slot < 0) {
+      if (n < g) {
+        uint16_t* orow = p.out + ((int64_t)b * p.hq + h * g + n) * D;
 #pragma unroll
-    for (int e = 0; e < W; ++e)
+        for (int r = 0; r < 4; ++r) {
+          uint16_t* dst = orow + W * (4 * G + r);
+          if constexpr (W == 8) {
+            u32x4 w4;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) sm_o[wave][n][W * (4 * G + r) + e] = sm.o[e][r];
-    if (G == 0) {
-      sm_m[wave][n] = sm.m;
-      sm_l[wave][n] = l_tot;
-    }
-    __syncthreads();
-    for (int idx = threadIdx.x; idx < g * D; idx += 256) {
-      const int hn = idx / D;
-      const int dd = idx - hn * D;
-      float M = sm_m[0][hn];
+            for (int i = 0; i < 4; ++i)
+              w4[i] = pack2<BF16>(sm.o[2 * i][r] * inv, sm.o[2 * i + 1][r] * inv);
+            *reinterpret_cast<u32x4*>(dst) = w4;
+          } else {
+            u32x2 w2;
 #pragma unroll
-      for (int w = 1; w < 4; ++w) M = fmaxf(M, sm_m[w][hn]);
-      float o = 0.f, lse2 = -INFINITY;
-      if (M != -INFINITY) {
-        float num = 0.f, den = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const float wt = exp2f(sm_m[w][hn] - M);
-          num += wt * sm_o[w][hn][dd];
-          den += wt * sm_l[w][hn];
+            for (int i = 0; i < 2; ++i)
+              w2[i] = pack2<BF16>(sm.o[2 * i][r] * inv, sm.o[2 * i + 1][r] * inv);
+            *reinterpret_cast<u32x2*>(dst) = w2;
+          }
         }
-        o = num / den;
-        lse2 = M + log2f(den);
+        if (p.lse && G == 0)
+          p.lse[(int64_t)b * p.hq + h * g + n] = lse2 * 0.69314718055994531f;
       }
-      const int head = h * g + hn;
-      if (slot < 0) {
-        p.out[((int64_t)b * p.hq + head) * D + dd] = f2h<BF16>(o);
-        if (p.lse && dd == 0)
-          p.lse[(int64_t)b * p.hq + head] = lse2 * 0.69314718055994531f;
-      } else {
-        p.partial_o[((int64_t)slot * p.hq + head) * D + dd] = o;
-        if (dd == 0) p.partial_lse[(int64_t)slot * p.hq + head] = lse2;
+    } else {
+      if (n < g) {
+        float* prow = p.partial_o + ((int64_t)slot * g + n) * D;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int e = 0; e < W; ++e) prow[W * (4 * G + r) + e] = sm.o[e][r] * inv;
+        if (G == 0) p.partial_lse[(int64_t)slot * g + n] = lse2;
+      }
+      // publish the partial, then count arrivals; the last arrival merges
+      __threadfence();
+      int prev = 0;
+      if (lane == 0) prev = atomicAdd(&p.counters[merge], 1);
+      prev = __shfl(prev, 0);
+      const int32_t* mp = reinterpret_cast<const int32_t*>(p.merges + merge);
+      const MergeItem mi{uniform(load_invariant(mp + 0)), uniform(load_invariant(mp + 1)),
+                         uniform(load_invariant(mp + 2)), uniform(load_invariant(mp + 3))};
+      if (prev == mi.nslots - 1) {
+        __threadfence();
+        merge_group<D, BF16>(p, mi, lane);
+        if (lane == 0) atomicExch(&p.counters[merge], 0);
       }
     }
-    __syncthreads();
   }
-}
-
-// Split-KV merge: o = sum_c 2^(lse_c - M) o_c / sum_c 2^(lse_c - M),
-// lse = M + log2(sum_c 2^(lse_c - M)) (base-2 partials, natural-log output).
-template <bool BF16>
-__global__ void __launch_bounds__(128)
-    decode_merge_kernel(const MergeItem* __restrict__ merges,
-                        const float* __restrict__ po,
-                        const float* __restrict__ pl, uint16_t* __restrict__ out,
-                        float* __restrict__ lse, int hq, int d) {
-  const MergeItem mi = merges[blockIdx.x];
-  const int head = blockIdx.y;
-  float M = -INFINITY;
-  for (int s = 0; s < mi.nslots; ++s)
-    M = fmaxf(M, pl[(int64_t)(mi.slot0 + s) * hq + head]);
-  float num = 0.f, den = 0.f;
-  const int dd = threadIdx.x;
-  if (M != -INFINITY) {
-    for (int s = 0; s < mi.nslots; ++s) {
-      const int64_t sh = (int64_t)(mi.slot0 + s) * hq + head;
-      const float wt = exp2f(pl[sh] - M);
-      den += wt;
-      if (dd < d) num += wt * po[sh * d + dd];
-    }
-  }
-  const float o = M != -INFINITY ? num / den : 0.f;
-  if (dd < d) out[((int64_t)mi.b * hq + head) * d + dd] = f2h<BF16>(o);
-  if (lse && dd == 0)
-    lse[(int64_t)mi.b * hq + head] =
-        M != -INFINITY ? (M + log2f(den)) * 0.69314718055994531f : -INFINITY;
 }
 
 // ----------------------------------------------------------------------------
@@ -483,25 +508,14 @@ static DecodeFn pick_decode(int d, bool bf16, bool fp8) {
   return fp8 ? decode_fn<128, false, true>() : decode_fn<128, false, false>();
 }
 
-// Resident decode workgroups per CU for the bf16 kernel of this head_dim
-// (the planner's slot count); PAGEDATTN_DECODE_WGS_PER_CU overrides it.
-static int decode_wgs_per_cu(int d) {
-  if (const char* env = std::getenv("PAGEDATTN_DECODE_WGS_PER_CU")) {
+// Waves the planner spreads the work over, per CU: two resident 4-wave
+// workgroups per CU; PAGEDATTN_DECODE_WAVES_PER_CU overrides it.
+static int decode_waves_per_cu() {
+  if (const char* env = std::getenv("PAGEDATTN_DECODE_WAVES_PER_CU")) {
     const int v = std::atoi(env);
     if (v > 0) return v;
   }
-  static int cached[2] = {0, 0};
-  int& c = cached[d == 128 ? 1 : 0];
-  if (c == 0) {
-    int nb = 0;
-    DecodeFn fn = pick_decode(d, true, false);
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &nb, reinterpret_cast<const void*>(fn), 256, 0) != hipSuccess ||
-        nb <= 0)
-      nb = 2;
-    c = nb;
-  }
-  return c;
+  return 8;
 }
 
 }  // namespace pa
@@ -533,6 +547,8 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   rc = validate_paged_metadata(who, kv_indptr_host, kv_last_page_len_host,
                                batch_size, page_size, &npages, &kv_len);
   if (rc) return rc;
+  const int hkv = num_kv_heads;
+  const int g = num_qo_heads / num_kv_heads;
 
   int64_t total = 0;
   int maxp = 0;
@@ -540,115 +556,127 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
     total += npages[b];
     maxp = std::max(maxp, npages[b]);
   }
+  int cus = device_cu_count();
+  if (cus <= 0) cus = 256;
+  const int64_t waves_max = std::max<int64_t>(1, (int64_t)cus * decode_waves_per_cu());
 
+  // items, grouped per wave
   std::vector<DecodeItem> items;
-  std::vector<int32_t> wg_ptr;
-  items.reserve(batch_size * 2 + 16);
-  // pieces per sequence, for slots / merges
-  std::vector<int32_t> first_piece(batch_size, -1), n_pieces(batch_size, 0);
-  auto add_piece = [&](int b, int lo, int hi) {
-    if (first_piece[b] < 0) first_piece[b] = (int)items.size();
-    n_pieces[b]++;
-    items.push_back(DecodeItem{b, lo, hi, -1});
+  std::vector<int32_t> wave_ptr(1, 0);
+  std::vector<int32_t> pieces((size_t)batch_size * hkv, 0);
+  auto make = [](int b, int h, int lo, int hi) {
+    return DecodeItem{b, h, lo, hi, -1, -1, 0, 0};
   };
-
   if (split_pages != 0) {
-    // fixed chunks (split_pages > 0) or whole sequences (< 0): one item per
-    // workgroup
-    const int chunk =
-        split_pages > 0 ? ((split_pages + 7) / 8) * 8 : std::max(1, maxp);
-    for (int b = 0; b < batch_size; ++b) {
-      if (npages[b] == 0) {
-        add_piece(b, 0, 0);
-        continue;
-      }
-      for (int lo = 0; lo < npages[b]; lo += chunk)
-        add_piece(b, lo, std::min(npages[b], lo + chunk));
-    }
-    // longest first
-    std::vector<int> order(items.size());
-    for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
-    std::stable_sort(order.begin(), order.end(), [&](int a, int c) {
-      return items[a].page_hi - items[a].page_lo >
-             items[c].page_hi - items[c].page_lo;
-    });
-    std::vector<DecodeItem> sorted(items.size());
-    for (size_t i = 0; i < order.size(); ++i) sorted[i] = items[order[i]];
-    // pieces of one sequence keep their relative order (first_piece stays a
-    // valid "has pieces" marker; slots are assigned below by sequence)
-    items.swap(sorted);
-    wg_ptr.resize(items.size() + 1);
-    for (size_t i = 0; i <= items.size(); ++i) wg_ptr[i] = (int32_t)i;
-  } else {
-    // balanced partition: every workgroup gets ~the same number of pages,
-    // cutting sequences at workgroup boundaries
-    int cus = device_cu_count();
-    if (cus <= 0) cus = 256;
-    const int64_t slots = (int64_t)cus * decode_wgs_per_cu(head_dim);
-    const int64_t x_max = std::max<int64_t>(1, slots / num_kv_heads);
-    int64_t target = (total + x_max - 1) / x_max;
-    target = std::max<int64_t>(8, ((target + 7) / 8) * 8);
-    int64_t fill = 0;
-    wg_ptr.push_back(0);
-    for (int b = 0; b < batch_size; ++b) {
-      if (npages[b] == 0) {
-        add_piece(b, 0, 0);
-        continue;
-      }
-      int lo = 0;
-      while (lo < npages[b]) {
-        const int take = (int)std::min<int64_t>(npages[b] - lo, target - fill);
-        add_piece(b, lo, lo + take);
-        lo += take;
-        fill += take;
-        if (fill == target) {
-          wg_ptr.push_back((int32_t)items.size());
-          fill = 0;
+    // fixed chunks (split_pages > 0) or whole sequences (< 0), assigned to
+    // waves longest-first onto the least-loaded wave
+    const int chunk = split_pages > 0 ? ((split_pages + 7) / 8) * 8 : INT32_MAX;
+    std::vector<DecodeItem> all;
+    for (int b = 0; b < batch_size; ++b)
+      for (int h = 0; h < hkv; ++h) {
+        if (npages[b] == 0) {
+          all.push_back(make(b, h, 0, 0));
+          pieces[(size_t)b * hkv + h]++;
+          continue;
+        }
+        for (int lo = 0; lo < npages[b]; lo += chunk) {
+          all.push_back(make(b, h, lo, (int)std::min<int64_t>(npages[b], (int64_t)lo + chunk)));
+          pieces[(size_t)b * hkv + h]++;
         }
       }
+    std::stable_sort(all.begin(), all.end(), [](const DecodeItem& a, const DecodeItem& c) {
+      return a.page_hi - a.page_lo > c.page_hi - c.page_lo;
+    });
+    const int64_t nw = std::min<int64_t>(waves_max, std::max<size_t>(1, all.size()));
+    std::vector<std::vector<int>> per_wave(nw);
+    std::priority_queue<std::pair<int64_t, int64_t>,
+                        std::vector<std::pair<int64_t, int64_t>>,
+                        std::greater<std::pair<int64_t, int64_t>>> heap;
+    for (int64_t w = 0; w < nw; ++w) heap.push({0, w});
+    for (size_t i = 0; i < all.size(); ++i) {
+      auto top = heap.top();
+      heap.pop();
+      per_wave[top.second].push_back((int)i);
+      top.first += std::max(1, all[i].page_hi - all[i].page_lo);
+      heap.push(top);
     }
-    if (wg_ptr.back() != (int32_t)items.size())
-      wg_ptr.push_back((int32_t)items.size());
+    for (auto& lst : per_wave) {
+      for (int i : lst) items.push_back(all[i]);
+      wave_ptr.push_back((int32_t)items.size());
+    }
+  } else {
+    // balanced: the (sequence, head, page) stream cut into equal shares
+    int64_t target = (total * hkv + waves_max - 1) / waves_max;
+    target = std::max<int64_t>(4, (target + 1) / 2 * 2);
+    int64_t fill = 0;
+    for (int b = 0; b < batch_size; ++b)
+      for (int h = 0; h < hkv; ++h) {
+        if (npages[b] == 0) {
+          items.push_back(make(b, h, 0, 0));
+          pieces[(size_t)b * hkv + h]++;
+          continue;
+        }
+        int lo = 0;
+        while (lo < npages[b]) {
+          const int take = (int)std::min<int64_t>(npages[b] - lo, target - fill);
+          items.push_back(make(b, h, lo, lo + take));
+          pieces[(size_t)b * hkv + h]++;
+          lo += take;
+          fill += take;
+          if (fill == target) {
+            wave_ptr.push_back((int32_t)items.size());
+            fill = 0;
+          }
+        }
+      }
+    if (wave_ptr.back() != (int32_t)items.size())
+      wave_ptr.push_back((int32_t)items.size());
   }
 
-  // slots for split sequences, merge items
+  // partial slots and merge groups for (sequence, head) pairs cut in pieces
   std::vector<MergeItem> merges;
+  std::vector<int32_t> group_of((size_t)batch_size * hkv, -1);
   int n_slots = 0;
-  {
-    std::vector<int32_t> slot0(batch_size, -1);
-    for (int b = 0; b < batch_size; ++b) {
-      if (n_pieces[b] > 1) {
-        slot0[b] = n_slots;
-        merges.push_back(MergeItem{b, n_slots, n_pieces[b], 0});
-        n_slots += n_pieces[b];
+  for (int b = 0; b < batch_size; ++b)
+    for (int h = 0; h < hkv; ++h) {
+      const int np = pieces[(size_t)b * hkv + h];
+      if (np > 1) {
+        group_of[(size_t)b * hkv + h] = (int)merges.size();
+        merges.push_back(MergeItem{b, h, n_slots, np});
+        n_slots += np;
       }
     }
-    std::vector<int32_t> next(batch_size, 0);
-    for (auto& it : items)
-      if (slot0[it.b] >= 0) it.slot = slot0[it.b] + next[it.b]++;
+  {
+    std::vector<int32_t> next(merges.size(), 0);
+    for (auto& it : items) {
+      const int grp = group_of[(size_t)it.b * hkv + it.h];
+      if (grp >= 0) {
+        it.merge = grp;
+        it.slot = merges[grp].slot0 + next[grp]++;
+      }
+    }
   }
 
   const int n_items = (int)items.size();
-  const int n_wg = (int)wg_ptr.size() - 1;
+  const int n_waves = (int)wave_ptr.size() - 1;
+  const size_t n_merge = merges.size();
   const size_t off_items = kWsHeader;
-  const size_t off_wg = ws_align(off_items + sizeof(DecodeItem) * n_items);
-  const size_t off_merge = ws_align(off_wg + sizeof(int32_t) * (n_wg + 1));
-  const size_t off_po = ws_align(off_merge + sizeof(MergeItem) * merges.size());
+  const size_t off_wave = ws_align(off_items + sizeof(DecodeItem) * n_items);
+  const size_t off_merge = ws_align(off_wave + sizeof(int32_t) * (n_waves + 1));
+  const size_t off_cnt = ws_align(off_merge + sizeof(MergeItem) * n_merge);
+  const size_t off_po = ws_align(off_cnt + sizeof(int32_t) * n_merge);
   const size_t off_pl =
-      ws_align(off_po + sizeof(float) * (size_t)n_slots * num_qo_heads * head_dim);
-  const size_t end = ws_align(off_pl + sizeof(float) * (size_t)n_slots * num_qo_heads);
-  const size_t host_bytes = off_po - kWsHeader;
+      ws_align(off_po + sizeof(float) * (size_t)n_slots * g * head_dim);
+  const size_t end = ws_align(off_pl + sizeof(float) * (size_t)n_slots * g);
+  const size_t host_bytes = off_po - kWsHeader;  // counters upload as zeros
 
   plan->host.assign(host_bytes / sizeof(int32_t), 0);
   char* hb = reinterpret_cast<char*>(plan->host.data());
   if (n_items)
-    std::memcpy(hb + (off_items - kWsHeader), items.data(),
-                sizeof(DecodeItem) * n_items);
-  std::memcpy(hb + (off_wg - kWsHeader), wg_ptr.data(),
-              sizeof(int32_t) * (n_wg + 1));
-  if (!merges.empty())
-    std::memcpy(hb + (off_merge - kWsHeader), merges.data(),
-                sizeof(MergeItem) * merges.size());
+    std::memcpy(hb + (off_items - kWsHeader), items.data(), sizeof(DecodeItem) * n_items);
+  std::memcpy(hb + (off_wave - kWsHeader), wave_ptr.data(), sizeof(int32_t) * (n_waves + 1));
+  if (n_merge)
+    std::memcpy(hb + (off_merge - kWsHeader), merges.data(), sizeof(MergeItem) * n_merge);
 
   plan->workspace = workspace;
   plan->workspace_bytes = workspace_bytes;
@@ -661,17 +689,18 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   plan->hkv = num_kv_heads;
   plan->d = head_dim;
   plan->page_size = page_size;
-  plan->n_items = n_wg;  // workgroups along x
-  plan->n_merge = (int)merges.size();
+  plan->n_items = n_waves;
+  plan->n_merge = (int)n_merge;
   plan->n_slots = n_slots;
   plan->split_pages = split_pages;
   plan->items_dev = ws + off_items;
+  plan->wave_ptr_dev = reinterpret_cast<const int32_t*>(ws + off_wave);
   plan->merge_dev = ws + off_merge;
+  plan->counters_dev = reinterpret_cast<int32_t*>(ws + off_cnt);
   plan->partial_o = reinterpret_cast<float*>(ws + off_po);
   plan->partial_lse = reinterpret_cast<float*>(ws + off_pl);
   plan->total_pages = total;
   plan->max_pages = maxp;
-  plan->wg_ptr_dev = reinterpret_cast<const int32_t*>(ws + off_wg);
   plan->mode = kPlanDecode;
   return PAGEDATTN_OK;
 }
@@ -699,22 +728,28 @@ int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
   if (fp8 && !kv_scales)
     return set_error(PAGEDATTN_ERR_INVALID, "%s: e4m3 pool needs kv_scales",
                      who);
-  if (plan->batch_size == 0) return PAGEDATTN_OK;
+  if (plan->batch_size == 0 || plan->n_items == 0) return PAGEDATTN_OK;
   if (!q || !paged_kv_cache || !kv_indices || !kv_indptr ||
       !kv_last_page_len || !out)
     return set_error(PAGEDATTN_ERR_INVALID, "%s: null pointer", who);
   if ((q_stride_n & 7) || (q_stride_h & 7) || !aligned16(q) ||
-      !aligned16(paged_kv_cache))
+      !aligned16(paged_kv_cache) || !aligned16(out))
     return set_error(PAGEDATTN_ERR_UNSUPPORTED,
-                     "%s: q and the pool must be 16-byte aligned with strides "
-                     "that are multiples of 8 elements",
+                     "%s: q, out and the pool must be 16-byte aligned with "
+                     "strides that are multiples of 8 elements",
                      who);
-  if (num_pages < 0)
-    return set_error(PAGEDATTN_ERR_INVALID, "%s: num_pages %d < 0", who,
-                     num_pages);
+  if (num_pages < 0 || num_indices < 0)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: negative sizes", who);
+
   DecodeParams p;
   p.items = static_cast<const DecodeItem*>(plan->items_dev);
-  p.wg_ptr = plan->wg_ptr_dev;
+  p.wave_ptr = plan->wave_ptr_dev;
+  p.merges = static_cast<const MergeItem*>(plan->merge_dev);
+  p.counters = plan->counters_dev;
+  p.n_waves = plan->n_items;
+  p.n_merge = plan->n_merge;
+  p.n_slots = plan->n_slots;
+  p.batch_size = plan->batch_size;
   p.q = static_cast<const uint16_t*>(q);
   p.q_sn = q_stride_n;
   p.q_sh = q_stride_h;
@@ -734,30 +769,10 @@ int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
   p.g = plan->hq / plan->hkv;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
 
-  hipStream_t s = (hipStream_t)stream;
-  const bool bf16 = q_dtype == PAGEDATTN_BF16;
-  DecodeFn fn = pick_decode(plan->d, bf16, fp8);
-  if (plan->n_items > 0) {
-    hipLaunchKernelGGL(fn, dim3(plan->n_items, plan->hkv), dim3(256), 0, s, p);
-    int rc = check_launch(who);
-    if (rc) return rc;
-  }
-  if (plan->n_merge > 0) {
-    const dim3 grid(plan->n_merge, plan->hq);
-    const dim3 block(plan->d);
-    if (bf16)
-      hipLaunchKernelGGL(decode_merge_kernel<true>, grid, block, 0, s,
-                         static_cast<const MergeItem*>(plan->merge_dev),
-                         plan->partial_o, plan->partial_lse, p.out, lse,
-                         plan->hq, plan->d);
-    else
-      hipLaunchKernelGGL(decode_merge_kernel<false>, grid, block, 0, s,
-                         static_cast<const MergeItem*>(plan->merge_dev),
-                         plan->partial_o, plan->partial_lse, p.out, lse,
-                         plan->hq, plan->d);
-    return check_launch("decode_run(merge)");
-  }
-  return PAGEDATTN_OK;
+  DecodeFn fn = pick_decode(plan->d, q_dtype == PAGEDATTN_BF16, fp8);
+  const int blocks = (plan->n_items + 3) / 4;
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, (hipStream_t)stream, p);
+  return check_launch(who);
 }
 
 }  // extern "C"
