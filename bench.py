@@ -78,13 +78,13 @@ def bench_decode(w, args, dev, dtype, label, cpu_sample: int = 0):
             for _ in range(reps)]
 
     def step(i, ev=None):
+        # the decode step: new token's K/V appended at kv_len - 1, then
+        # attention, in one launch (pagedattn_decode_run_append)
         t = inst[i % reps]
-        pagedattn.append_paged_kv_cache(t.k_new, t.v_new, t.batch_indices, t.positions, t.pool,
-                                        t.kv_indices, t.kv_indptr, t.kv_last_page_len,
-                                        kv_layout="HND", kv_scales=t.scales)
         if ev is not None:
             ev[0].record()
-        dw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps])
+        dw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps], append_key=t.k_new,
+               append_value=t.v_new)
         if ev is not None:
             ev[1].record()
 

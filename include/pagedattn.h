@@ -161,6 +161,25 @@ int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
                          const int32_t* kv_last_page_len, void* out,
                          float* lse, float sm_scale, void* stream);
 
+/* The decode step of the engine (src/models/llama.py:184-245 in decode mode,
+ * metadata from src/engine/runtime/step_executor.py:220-225) in one launch:
+ * flashinfer.append_paged_kv_cache(append_key, append_value,
+ * batch_indices = arange(B), positions = kv_len - 1, ...) followed by
+ * BatchDecodeWithPagedKVCacheWrapper.forward.  append_key / append_value
+ * [B, num_kv_heads, head_dim] (q dtype, strided) are written into slot
+ * kv_len_b - 1 of each sequence's last page (e4m3 pools: round(clamp(x /
+ * scale, +-448)) with that page's scale) and take part in the attention.
+ * Same plan, pool and output contract as pagedattn_decode_run. */
+int pagedattn_decode_run_append(
+    const pagedattn_plan* plan, const void* q, int64_t q_stride_n,
+    int64_t q_stride_h, int32_t q_dtype, const void* append_key,
+    const void* append_value, int64_t k_stride_n, int64_t k_stride_h,
+    int64_t v_stride_n, int64_t v_stride_h, void* paged_kv_cache,
+    int32_t kv_dtype, const float* kv_scales, int32_t num_pages,
+    const int32_t* kv_indices, int32_t num_indices, const int32_t* kv_indptr,
+    const int32_t* kv_last_page_len, void* out, float* lse, float sm_scale,
+    void* stream);
+
 /* BatchPrefillWithPagedKVCacheWrapper.begin_forward(qo_indptr, kv_indptr,
  *     kv_indices, kv_last_page_len, Hq, Hkv, D, page_size, q_data_type)
  *     (src/models/llama.py:86-116).  Host copies of the indptr arrays. */

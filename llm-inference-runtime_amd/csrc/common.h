@@ -50,17 +50,25 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
                                            (int)bytes, kRsrcWord3);
 }
 
+// Cache policy of buffer loads: kCachePolicyStream marks data read once
+// (K/V pages of a decode pass) as non-temporal.
+constexpr int kCachePolicyDefault = 0;
+constexpr int kCachePolicyStream = 2;
+
+template <int POLICY = kCachePolicyDefault>
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r,
                                             uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POLICY);
 }
+template <int POLICY = kCachePolicyDefault>
 __device__ __forceinline__ u32x2 buf_load8(__amdgpu_buffer_rsrc_t r,
                                            uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, POLICY);
 }
+template <int POLICY = kCachePolicyDefault>
 __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r,
                                               uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, POLICY);
 }
 
 __device__ __forceinline__ int uniform(int x) {

@@ -6,10 +6,9 @@
 // each K/V byte is read from HBM once.  Waves are independent: no barriers,
 // no cross-wave LDS merges, so one slow memory request stalls one wave only.
 // The host planner cuts the concatenated (sequence, head, page) stream into
-// equal shares per wave; sequences cut at a share boundary write split
-// partials, and the last of a group's waves to finish merges them (an
-// arrival counter in the workspace, released/acquired with device-scope
-// fences), so one launch produces the final output.
+// equal shares per wave (or assigns whole sequences / fixed chunks to the
+// least-loaded wave); sequences cut in pieces write split partials that a
+// small merge launch combines.
 //
 // Per page pair (32 tokens) a wave does:
 //   S^T[32 tok x 16 heads] = K[tok x D] . Q^T      (v_mfma_f32_16x16x32, D/32 k-steps per page)
@@ -45,8 +44,6 @@ namespace pa {
 struct DecodeParams {
   const DecodeItem* items;
   const int32_t* wave_ptr;  // [n_waves + 1]: items of wave w
-  const MergeItem* merges;
-  int32_t* counters;        // [n_merge] arrival counters (0 between launches)
   int32_t n_waves, n_merge, n_slots, batch_size;
   const uint16_t* q;
   int64_t q_sn, q_sh;
@@ -63,7 +60,16 @@ struct DecodeParams {
   float* partial_lse;  // [n_slots, g] (base 2)
   int32_t hq, hkv, g;
   float scale_log2;  // sm_scale * log2(e)
+  // fused append (decode_run_append only): row b of k_new / v_new
+  // [B, Hkv, D] is sequence b's newest token, position kv_len_b - 1
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int64_t k_sn, k_sh, v_sn, v_sh;
 };
+
+#ifndef DECODE_KV_POLICY
+#define DECODE_KV_POLICY kCachePolicyStream
+#endif
 
 template <int N>
 struct RawT;
@@ -72,7 +78,7 @@ struct RawT<16> {
   using type = u32x4;
   static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r,
                                               uint32_t off) {
-    return buf_load16(r, off);
+    return buf_load16<DECODE_KV_POLICY>(r, off);
   }
 };
 template <>
@@ -80,7 +86,7 @@ struct RawT<8> {
   using type = u32x2;
   static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r,
                                               uint32_t off) {
-    return buf_load8(r, off);
+    return buf_load8<DECODE_KV_POLICY>(r, off);
   }
 };
 template <>
@@ -88,7 +94,7 @@ struct RawT<4> {
   using type = uint32_t;
   static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r,
                                               uint32_t off) {
-    return buf_load4(r, off);
+    return buf_load4<DECODE_KV_POLICY>(r, off);
   }
 };
 
@@ -236,7 +242,7 @@ struct SoftmaxState {
 };
 
 template <int D, bool BF16, bool FP8>
-__device__ __forceinline__ void compute_pair(const Stage<D, BF16, FP8>& st,
+__device__ __forceinline__ void compute_pair(Stage<D, BF16, FP8>& st,
                                              const u32x4 (&qf)[D / 32],
                                              SoftmaxState<D, BF16, FP8>& sm,
                                              float scale_log2, int G) {
@@ -334,37 +340,123 @@ __device__ __forceinline__ void compute_pair(const Stage<D, BF16, FP8>& st,
   }
 }
 
-// Merge of one split group by the last wave to finish:
-// o = sum_c 2^(lse_c - M) o_c / sum_c 2^(lse_c - M), lse = M + log2(sum ...).
-template <int D, bool BF16>
-__device__ __forceinline__ void merge_group(const DecodeParams& p,
-                                            const MergeItem& mi, int lane) {
-  const int g = p.g;
-  for (int idx = lane; idx < g * D; idx += kWave) {
-    const int hn = idx / D;
-    const int dd = idx - hn * D;
-    float M = -INFINITY;
-    for (int s = 0; s < mi.nslots; ++s)
-      M = fmaxf(M, p.partial_lse[(int64_t)(mi.slot0 + s) * g + hn]);
-    float num = 0.f, den = 0.f;
-    if (M != -INFINITY) {
-      for (int s = 0; s < mi.nslots; ++s) {
-        const int64_t sh = (int64_t)(mi.slot0 + s) * g + hn;
-        const float wt = exp2f(p.partial_lse[sh] - M);
-        den += wt;
-        num += wt * p.partial_o[sh * D + dd];
-      }
+// New-token row of the fused append, held in the lanes that own it in the
+// stage layouts: K lanes with n == slot hold d = 32 ks + 8 G; V lanes with
+// G == slot / 4 hold d in [W n, W n + W).  Values are the bits stored in the
+// pool (e4m3 pools: quantised with the page's scale).
+template <int D, bool BF16, bool FP8>
+struct NewRow {
+  using Tr = DecodeTraits<D, BF16, FP8>;
+  typename Tr::KRaw k[Tr::KS];
+  typename Tr::VRaw v;
+};
+
+template <int N>
+__device__ __forceinline__ typename RawT<N>::type load_raw16(const uint16_t* src);
+template <>
+__device__ __forceinline__ u32x4 load_raw16<16>(const uint16_t* src) {
+  return *reinterpret_cast<const u32x4*>(src);
+}
+template <>
+__device__ __forceinline__ u32x2 load_raw16<8>(const uint16_t* src) {
+  return *reinterpret_cast<const u32x2*>(src);
+}
+
+// 8 sixteen-bit values -> 8 e4m3 bytes, round(clamp(x / scale, +-448)).
+template <bool BF16>
+__device__ __forceinline__ u32x2 quant8(u32x4 x, float scale) {
+  float f[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = h2f<BF16>((uint16_t)(x[e] & 0xffffu));
+    f[2 * e + 1] = h2f<BF16>((uint16_t)(x[e] >> 16));
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / scale, -448.f), 448.f);
+  u32x2 o;
+  o[0] = f32_to_e4m3x4(f[0], f[1], f[2], f[3]);
+  o[1] = f32_to_e4m3x4(f[4], f[5], f[6], f[7]);
+  return o;
+}
+template <bool BF16>
+__device__ __forceinline__ uint32_t quant4(u32x2 x, float scale) {
+  float f[4];
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    f[2 * e] = h2f<BF16>((uint16_t)(x[e] & 0xffffu));
+    f[2 * e + 1] = h2f<BF16>((uint16_t)(x[e] >> 16));
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) f[e] = fminf(fmaxf(f[e] / scale, -448.f), 448.f);
+  return f32_to_e4m3x4(f[0], f[1], f[2], f[3]);
+}
+
+// Loads sequence b / head h's new row into the owning lanes and writes it to
+// slot `slot` of page `page` (the append of flashinfer.append_paged_kv_cache
+// at position kv_len - 1).
+template <int D, bool BF16, bool FP8>
+__device__ __forceinline__ void fused_append(const DecodeParams& p,
+                                             NewRow<D, BF16, FP8>& nr, int b,
+                                             int h, int page, int slot, int n,
+                                             int G) {
+  using Tr = DecodeTraits<D, BF16, FP8>;
+  constexpr int W = Tr::W;
+  const uint16_t* krow = p.k_new + (int64_t)b * p.k_sn + (int64_t)h * p.k_sh;
+  const uint16_t* vrow = p.v_new + (int64_t)b * p.v_sn + (int64_t)h * p.v_sh;
+  uint8_t* kdst = const_cast<uint8_t*>(p.cache) +
+                  ((int64_t)page * 2 * p.hkv + h) * (int64_t)Tr::PAGE_BYTES +
+                  (int64_t)slot * D * Tr::ESZ;
+  uint8_t* vdst = kdst + (int64_t)p.hkv * Tr::PAGE_BYTES;
+  float ks_ = 1.f, vs_ = 1.f;
+  if constexpr (FP8) {
+    const int64_t si = ((int64_t)page * 2) * p.hkv + h;
+    ks_ = load_invariant(p.kv_scales + si);
+    vs_ = load_invariant(p.kv_scales + si + p.hkv);
+  }
+#pragma unroll
+  for (int kk = 0; kk < Tr::KS; ++kk) {
+    const u32x4 x = *reinterpret_cast<const u32x4*>(krow + 32 * kk + 8 * G);
+    if constexpr (FP8) {
+      nr.k[kk] = quant8<BF16>(x, ks_);
+    } else {
+      nr.k[kk] = x;
     }
-    const int head = mi.h * g + hn;
-    p.out[((int64_t)mi.b * p.hq + head) * D + dd] =
-        f2h<BF16>(M != -INFINITY ? num / den : 0.f);
-    if (p.lse && dd == 0)
-      p.lse[(int64_t)mi.b * p.hq + head] =
-          M != -INFINITY ? (M + log2f(den)) * 0.69314718055994531f : -INFINITY;
+    if (n == slot)
+      *reinterpret_cast<typename Tr::KRaw*>(kdst + (32 * kk + 8 * G) * Tr::ESZ) = nr.k[kk];
+  }
+  const auto vx = load_raw16<W * 2>(vrow + W * n);
+  if constexpr (FP8) {
+    if constexpr (W == 8) {
+      nr.v = quant8<BF16>(vx, vs_);
+    } else {
+      nr.v = quant4<BF16>(vx, vs_);
+    }
+  } else {
+    nr.v = vx;
+  }
+  if (G == (slot >> 2))
+    *reinterpret_cast<typename Tr::VRaw*>(vdst + W * n * Tr::ESZ) = nr.v;
+}
+
+// Replace the stale slot of the new token in a loaded stage (page half pi).
+template <int D, bool BF16, bool FP8>
+__device__ __forceinline__ void patch_stage(Stage<D, BF16, FP8>& st,
+                                            const NewRow<D, BF16, FP8>& nr,
+                                            int pi, int slot, int n, int G) {
+  using Tr = DecodeTraits<D, BF16, FP8>;
+#pragma unroll
+  for (int pj = 0; pj < 2; ++pj) {
+    if (pj != pi) continue;
+#pragma unroll
+    for (int kk = 0; kk < Tr::KS; ++kk)
+      if (n == slot) st.k[pj][kk] = nr.k[kk];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      if (G == (slot >> 2) && r == (slot & 3)) st.v[4 * pj + r] = nr.v;
   }
 }
 
-template <int D, bool BF16, bool FP8>
+template <int D, bool BF16, bool FP8, bool APPEND>
 __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
@@ -412,6 +504,20 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
       }
     }
 
+    // the item that holds the sequence's last page also performs the append
+    NewRow<D, BF16, FP8> nr;
+    int new_pg = -1;  // page index (within the sequence) of the new token
+    const int new_slot = last - 1;
+    if constexpr (APPEND) {
+      if (npages > 0 && npages - 1 >= page_lo && npages - 1 < page_hi) {
+        const int page = page_id(p, ind_lo, npages - 1, npages);
+        if (page >= 0) {
+          new_pg = npages - 1;
+          fused_append(p, nr, b, h, page, new_slot, n, G);
+        }
+      }
+    }
+
     SoftmaxState<D, BF16, FP8> sm;
 #pragma unroll
     for (int e = 0; e < W; ++e) sm.o[e] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -428,10 +534,18 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
       for (int i = 0; i < n_pairs; i += 2) {
         const PairIds id_a = fetch_ids(p, ind_lo, page_lo + 2 * (i + 2), page_hi);
         load_pair(sb, p, h, id_b, page_lo + 2 * (i + 1), npages, last, n, G);
+        if constexpr (APPEND) {
+          const int d_pg = new_pg - (page_lo + 2 * i);
+          if (new_pg >= 0 && d_pg >= 0 && d_pg < 2) patch_stage(sa, nr, d_pg, new_slot, n, G);
+        }
         compute_pair(sa, qf, sm, p.scale_log2, G);
         if (i + 1 >= n_pairs) break;
         id_b = fetch_ids(p, ind_lo, page_lo + 2 * (i + 3), page_hi);
         load_pair(sa, p, h, id_a, page_lo + 2 * (i + 2), npages, last, n, G);
+        if constexpr (APPEND) {
+          const int d_pg = new_pg - (page_lo + 2 * (i + 1));
+          if (new_pg >= 0 && d_pg >= 0 && d_pg < 2) patch_stage(sb, nr, d_pg, new_slot, n, G);
+        }
         compute_pair(sb, qf, sm, p.scale_log2, G);
       }
     }
@@ -473,21 +587,43 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
           for (int e = 0; e < W; ++e) prow[W * (4 * G + r) + e] = sm.o[e][r] * inv;
         if (G == 0) p.partial_lse[(int64_t)slot * g + n] = lse2;
       }
-      // publish the partial, then count arrivals; the last arrival merges
-      __threadfence();
-      int prev = 0;
-      if (lane == 0) prev = atomicAdd(&p.counters[merge], 1);
-      prev = __shfl(prev, 0);
-      const int32_t* mp = reinterpret_cast<const int32_t*>(p.merges + merge);
-      const MergeItem mi{uniform(load_invariant(mp + 0)), uniform(load_invariant(mp + 1)),
-                         uniform(load_invariant(mp + 2)), uniform(load_invariant(mp + 3))};
-      if (prev == mi.nslots - 1) {
-        __threadfence();
-        merge_group<D, BF16>(p, mi, lane);
-        if (lane == 0) atomicExch(&p.counters[merge], 0);
-      }
     }
   }
+}
+
+// Split-KV merge, one workgroup per (split group, query head):
+// o = sum_c 2^(lse_c - M) o_c / sum_c 2^(lse_c - M),
+// lse = M + log2(sum_c 2^(lse_c - M)) (base-2 partials, natural-log output).
+// A separate launch: the kernel boundary orders the partial writes before
+// these reads across the XCDs' L2 caches without per-item cache flushes.
+template <bool BF16>
+__global__ void __launch_bounds__(128)
+    decode_merge_kernel(const MergeItem* __restrict__ merges,
+                        const float* __restrict__ po,
+                        const float* __restrict__ pl, uint16_t* __restrict__ out,
+                        float* __restrict__ lse, int hq, int g, int d) {
+  const MergeItem mi = merges[blockIdx.x];
+  const int hn = blockIdx.y;  // query head within the group
+  const int head = mi.h * g + hn;
+  float M = -INFINITY;
+  for (int s = 0; s < mi.nslots; ++s)
+    M = fmaxf(M, pl[(int64_t)(mi.slot0 + s) * g + hn]);
+  float num = 0.f, den = 0.f;
+  const int dd = threadIdx.x;
+  if (M != -INFINITY) {
+    for (int s = 0; s < mi.nslots; ++s) {
+      const int64_t sh = (int64_t)(mi.slot0 + s) * g + hn;
+      const float wt = exp2f(pl[sh] - M);
+      den += wt;
+      if (dd < d) num += wt * po[sh * d + dd];
+    }
+  }
+  if (dd < d)
+    out[((int64_t)mi.b * hq + head) * d + dd] =
+        f2h<BF16>(M != -INFINITY ? num / den : 0.f);
+  if (lse && dd == 0)
+    lse[(int64_t)mi.b * hq + head] =
+        M != -INFINITY ? (M + log2f(den)) * 0.69314718055994531f : -INFINITY;
 }
 
 // ----------------------------------------------------------------------------
@@ -495,27 +631,28 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
 using DecodeFn = void (*)(DecodeParams);
 
 template <int D, bool BF16, bool FP8>
-DecodeFn decode_fn() {
-  return decode_kernel<D, BF16, FP8>;
+DecodeFn decode_fn(bool append) {
+  return append ? decode_kernel<D, BF16, FP8, true> : decode_kernel<D, BF16, FP8, false>;
 }
 
-static DecodeFn pick_decode(int d, bool bf16, bool fp8) {
+static DecodeFn pick_decode(int d, bool bf16, bool fp8, bool append) {
   if (d == 64) {
-    if (bf16) return fp8 ? decode_fn<64, true, true>() : decode_fn<64, true, false>();
-    return fp8 ? decode_fn<64, false, true>() : decode_fn<64, false, false>();
+    if (bf16) return fp8 ? decode_fn<64, true, true>(append) : decode_fn<64, true, false>(append);
+    return fp8 ? decode_fn<64, false, true>(append) : decode_fn<64, false, false>(append);
   }
-  if (bf16) return fp8 ? decode_fn<128, true, true>() : decode_fn<128, true, false>();
-  return fp8 ? decode_fn<128, false, true>() : decode_fn<128, false, false>();
+  if (bf16) return fp8 ? decode_fn<128, true, true>(append) : decode_fn<128, true, false>(append);
+  return fp8 ? decode_fn<128, false, true>(append) : decode_fn<128, false, false>(append);
 }
 
-// Waves the planner spreads the work over, per CU: two resident 4-wave
-// workgroups per CU; PAGEDATTN_DECODE_WAVES_PER_CU overrides it.
+// Waves the planner spreads the work over, per CU (one wave per SIMD keeps
+// enough loads in flight with two register stages);
+// PAGEDATTN_DECODE_WAVES_PER_CU overrides it.
 static int decode_waves_per_cu() {
   if (const char* env = std::getenv("PAGEDATTN_DECODE_WAVES_PER_CU")) {
     const int v = std::atoi(env);
     if (v > 0) return v;
   }
-  return 8;
+  return 4;
 }
 
 }  // namespace pa
@@ -663,12 +800,11 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   const size_t off_items = kWsHeader;
   const size_t off_wave = ws_align(off_items + sizeof(DecodeItem) * n_items);
   const size_t off_merge = ws_align(off_wave + sizeof(int32_t) * (n_waves + 1));
-  const size_t off_cnt = ws_align(off_merge + sizeof(MergeItem) * n_merge);
-  const size_t off_po = ws_align(off_cnt + sizeof(int32_t) * n_merge);
+  const size_t off_po = ws_align(off_merge + sizeof(MergeItem) * n_merge);
   const size_t off_pl =
       ws_align(off_po + sizeof(float) * (size_t)n_slots * g * head_dim);
   const size_t end = ws_align(off_pl + sizeof(float) * (size_t)n_slots * g);
-  const size_t host_bytes = off_po - kWsHeader;  // counters upload as zeros
+  const size_t host_bytes = off_po - kWsHeader;
 
   plan->host.assign(host_bytes / sizeof(int32_t), 0);
   char* hb = reinterpret_cast<char*>(plan->host.data());
@@ -696,7 +832,6 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   plan->items_dev = ws + off_items;
   plan->wave_ptr_dev = reinterpret_cast<const int32_t*>(ws + off_wave);
   plan->merge_dev = ws + off_merge;
-  plan->counters_dev = reinterpret_cast<int32_t*>(ws + off_cnt);
   plan->partial_o = reinterpret_cast<float*>(ws + off_po);
   plan->partial_lse = reinterpret_cast<float*>(ws + off_pl);
   plan->total_pages = total;
@@ -705,15 +840,27 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   return PAGEDATTN_OK;
 }
 
-int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
-                         int64_t q_stride_n, int64_t q_stride_h,
-                         int32_t q_dtype, const void* paged_kv_cache,
-                         int32_t kv_dtype, const float* kv_scales,
-                         int32_t num_pages, const int32_t* kv_indices,
-                         int32_t num_indices, const int32_t* kv_indptr,
-                         const int32_t* kv_last_page_len, void* out,
-                         float* lse, float sm_scale, void* stream) {
-  const char* who = "decode_run";
+}  // extern "C"
+
+namespace pa {
+
+struct AppendRows {
+  const void* k;
+  const void* v;
+  int64_t k_sn, k_sh, v_sn, v_sh;
+  int32_t dtype;
+};
+
+static int decode_run_impl(const char* who, const pagedattn_plan* plan,
+                           const void* q, int64_t q_stride_n,
+                           int64_t q_stride_h, int32_t q_dtype,
+                           const void* paged_kv_cache, int32_t kv_dtype,
+                           const float* kv_scales, int32_t num_pages,
+                           const int32_t* kv_indices, int32_t num_indices,
+                           const int32_t* kv_indptr,
+                           const int32_t* kv_last_page_len, void* out,
+                           float* lse, float sm_scale, const AppendRows* app,
+                           void* stream) {
   if (!plan || plan->mode != kPlanDecode)
     return set_error(PAGEDATTN_ERR_PLAN, "%s: no decode plan (call plan first)",
                      who);
@@ -744,8 +891,6 @@ int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
   DecodeParams p;
   p.items = static_cast<const DecodeItem*>(plan->items_dev);
   p.wave_ptr = plan->wave_ptr_dev;
-  p.merges = static_cast<const MergeItem*>(plan->merge_dev);
-  p.counters = plan->counters_dev;
   p.n_waves = plan->n_items;
   p.n_merge = plan->n_merge;
   p.n_slots = plan->n_slots;
@@ -768,11 +913,75 @@ int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
   p.hkv = plan->hkv;
   p.g = plan->hq / plan->hkv;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
+  p.k_new = app ? static_cast<const uint16_t*>(app->k) : nullptr;
+  p.v_new = app ? static_cast<const uint16_t*>(app->v) : nullptr;
+  p.k_sn = app ? app->k_sn : 0;
+  p.k_sh = app ? app->k_sh : 0;
+  p.v_sn = app ? app->v_sn : 0;
+  p.v_sh = app ? app->v_sh : 0;
 
-  DecodeFn fn = pick_decode(plan->d, q_dtype == PAGEDATTN_BF16, fp8);
+  hipStream_t s = (hipStream_t)stream;
+  const bool bf16 = q_dtype == PAGEDATTN_BF16;
+  DecodeFn fn = pick_decode(plan->d, bf16, fp8, app != nullptr);
   const int blocks = (plan->n_items + 3) / 4;
-  hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, (hipStream_t)stream, p);
-  return check_launch(who);
+  hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, s, p);
+  int rc = check_launch(who);
+  if (rc || plan->n_merge == 0) return rc;
+  const dim3 grid(plan->n_merge, p.g);
+  const MergeItem* merges = static_cast<const MergeItem*>(plan->merge_dev);
+  if (bf16)
+    hipLaunchKernelGGL(decode_merge_kernel<true>, grid, dim3(plan->d), 0, s, merges,
+                       plan->partial_o, plan->partial_lse, p.out, lse, plan->hq, p.g,
+                       plan->d);
+  else
+    hipLaunchKernelGGL(decode_merge_kernel<false>, grid, dim3(plan->d), 0, s, merges,
+                       plan->partial_o, plan->partial_lse, p.out, lse, plan->hq, p.g,
+                       plan->d);
+  return check_launch("decode_run(merge)");
+}
+
+}  // namespace pa
+
+extern "C" {
+
+int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
+                         int64_t q_stride_n, int64_t q_stride_h,
+                         int32_t q_dtype, const void* paged_kv_cache,
+                         int32_t kv_dtype, const float* kv_scales,
+                         int32_t num_pages, const int32_t* kv_indices,
+                         int32_t num_indices, const int32_t* kv_indptr,
+                         const int32_t* kv_last_page_len, void* out,
+                         float* lse, float sm_scale, void* stream) {
+  return decode_run_impl("decode_run", plan, q, q_stride_n, q_stride_h, q_dtype,
+                         paged_kv_cache, kv_dtype, kv_scales, num_pages,
+                         kv_indices, num_indices, kv_indptr, kv_last_page_len,
+                         out, lse, sm_scale, nullptr, stream);
+}
+
+int pagedattn_decode_run_append(
+    const pagedattn_plan* plan, const void* q, int64_t q_stride_n,
+    int64_t q_stride_h, int32_t q_dtype, const void* append_key,
+    const void* append_value, int64_t k_stride_n, int64_t k_stride_h,
+    int64_t v_stride_n, int64_t v_stride_h, void* paged_kv_cache,
+    int32_t kv_dtype, const float* kv_scales, int32_t num_pages,
+    const int32_t* kv_indices, int32_t num_indices, const int32_t* kv_indptr,
+    const int32_t* kv_last_page_len, void* out, float* lse, float sm_scale,
+    void* stream) {
+  const char* who = "decode_run_append";
+  if (!append_key || !append_value)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: null append rows", who);
+  if ((k_stride_n & 7) || (k_stride_h & 7) || (v_stride_n & 7) ||
+      (v_stride_h & 7) || !aligned16(append_key) || !aligned16(append_value))
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                     "%s: append rows must be 16-byte aligned with strides that "
+                     "are multiples of 8 elements",
+                     who);
+  AppendRows app{append_key, append_value, k_stride_n, k_stride_h,
+                 v_stride_n, v_stride_h, q_dtype};
+  return decode_run_impl(who, plan, q, q_stride_n, q_stride_h, q_dtype,
+                         paged_kv_cache, kv_dtype, kv_scales, num_pages,
+                         kv_indices, num_indices, kv_indptr, kv_last_page_len,
+                         out, lse, sm_scale, &app, stream);
 }
 
 }  // extern "C"

@@ -24,7 +24,7 @@ struct DecodeItem {
 };
 
 // Split-KV merge group: (sequence b, KV head h) owns partial slots
-// [slot0, slot0 + nslots); the last of its items to finish merges them.
+// [slot0, slot0 + nslots).
 struct MergeItem {
   int32_t b, h, slot0, nslots;
 };
@@ -57,7 +57,6 @@ struct pagedattn_plan {
   void* items_dev = nullptr;
   const int32_t* wave_ptr_dev = nullptr;  // decode: items of wave w
   void* merge_dev = nullptr;
-  int32_t* counters_dev = nullptr;  // decode: one arrival counter per merge group
   float* partial_o = nullptr;
   float* partial_lse = nullptr;
   void* workspace = nullptr;

@@ -67,6 +67,10 @@ _SIGNATURES = {
         _c_int,
         [_c_p, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_int, _c_p, _c_int,
          _c_p, _c_int, _c_p, _c_p, _c_p, _c_p, _c_f, _c_p]),
+    "pagedattn_decode_run_append": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_p, _c_int, _c_p, _c_int, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p, _c_f, _c_p]),
     "pagedattn_prefill_plan": (
         _c_int,
         [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_int,

@@ -311,7 +311,12 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
     def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, *,
             kv_scales: torch.Tensor | None = None, out: torch.Tensor | None = None,
             lse: torch.Tensor | None = None, return_lse: bool = False,
-            sm_scale: float | None = None):
+            sm_scale: float | None = None, append_key: torch.Tensor | None = None,
+            append_value: torch.Tensor | None = None):
+        """Decode attention.  With append_key/append_value ([B, Hkv, D], the
+        newest token of every sequence, position kv_len - 1) the page append
+        of the decode step runs inside the same launch (the engine's decode
+        step: batch_indices = arange(B), positions = kv_len - 1)."""
         if not self._planned:
             raise RuntimeError("plan()/begin_forward() must be called before run()/forward()")
         num_pages, _, _ = _check_pool(paged_kv_cache, self._hkv, self._d, self._kv_layout)
@@ -330,11 +335,23 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
         scale = sm_scale if sm_scale is not None else self._sm_scale
         if scale is None:
             scale = 1.0 / math.sqrt(self._d)
-        call("pagedattn_decode_run", self._plan.handle, ptr(q), q.stride(0), q.stride(1),
-             dtype_code(q.dtype), ptr(paged_kv_cache), dtype_code(paged_kv_cache.dtype),
-             ptr(scales), num_pages, ptr(self._indices), self._indices.numel(),
-             ptr(self._indptr), ptr(self._last), ptr(out), ptr(lse), float(scale),
-             _stream(q.device))
+        common = (ptr(paged_kv_cache), dtype_code(paged_kv_cache.dtype), ptr(scales),
+                  num_pages, ptr(self._indices), self._indices.numel(), ptr(self._indptr),
+                  ptr(self._last), ptr(out), ptr(lse), float(scale), _stream(q.device))
+        if append_key is None and append_value is None:
+            call("pagedattn_decode_run", self._plan.handle, ptr(q), q.stride(0), q.stride(1),
+                 dtype_code(q.dtype), *common)
+        else:
+            if append_key is None or append_value is None:
+                raise ValueError("append_key and append_value go together")
+            for name, t in (("append_key", append_key), ("append_value", append_value)):
+                _check_rows(t, name, self._hkv, self._d)
+                if t.shape[0] != self._bsz or t.dtype != q.dtype:
+                    raise ValueError(f"{name} must be [batch, num_kv_heads, head_dim] in q's dtype")
+            call("pagedattn_decode_run_append", self._plan.handle, ptr(q), q.stride(0),
+                 q.stride(1), dtype_code(q.dtype), ptr(append_key), ptr(append_value),
+                 append_key.stride(0), append_key.stride(1), append_value.stride(0),
+                 append_value.stride(1), *common)
         return (out, lse) if return_lse else out
 
     def forward(self, q: torch.Tensor, paged_kv_cache: torch.Tensor,

@@ -159,3 +159,57 @@ def test_decode_e4m3(gpu, d, hq, hkv):
                               kv_scales=scales)
         assert max_err(out, ref_o) <= TOL_FP8, split
         assert lse_err(lse, ref_l) <= TOL_LSE
+
+
+@pytest.mark.parametrize("d,hq,hkv,fp8", [(64, 32, 4, False), (128, 32, 8, False),
+                                          (128, 64, 8, True), (64, 32, 4, True)])
+def test_decode_fused_append_equals_separate(gpu, d, hq, hkv, fp8):
+    # one launch (append at kv_len - 1 + attention) == append kernel + decode
+    meta, pool, q = decode_case(gpu, EDGE_LENS, hq, hkv, d, seed=33)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(34)
+    kn = torch.randn((len(EDGE_LENS), hkv, d), generator=g, device=gpu).to(torch.bfloat16) * 3
+    vn = torch.randn((len(EDGE_LENS), hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+    scales = None
+    if fp8:
+        pool, scales = pagedattn.quantize_pages_e4m3(pool)
+    pool_a, pool_b = pool.clone(), pool.clone()
+    ws = workspace(gpu)
+    for split in (-1, 0, 8):
+        pa_, pb_ = pool_a.clone(), pool_b.clone()
+        pagedattn.append_paged_kv_cache(kn, vn, i32(meta.batch_indices, gpu),
+                                        i32(meta.positions, gpu), pa_,
+                                        i32(meta.kv_indices, gpu), i32(meta.kv_indptr, gpu),
+                                        i32(meta.kv_last_page_len, gpu), kv_layout="HND",
+                                        kv_scales=scales)
+        w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+        w.plan(i32(meta.kv_indptr, gpu), i32(meta.kv_indices, gpu),
+               i32(meta.kv_last_page_len, gpu), hq, hkv, d, 16, q_data_type=torch.bfloat16,
+               split_pages=split)
+        o_sep, l_sep = w.run(q, pa_, kv_scales=scales, return_lse=True)
+        o_fus, l_fus = w.run(q, pb_, kv_scales=scales, return_lse=True, append_key=kn,
+                             append_value=vn)
+        torch.cuda.synchronize()
+        assert np.array_equal(O.to_bits(pa_), O.to_bits(pb_)), split
+        assert torch.equal(o_sep, o_fus), split
+        assert torch.equal(l_sep, l_fus), split
+    ref_o, _ = oracle_decode(meta, pb_, q, scales=scales)
+    assert max_err(o_fus, ref_o) <= (TOL_FP8 if fp8 else TOL_BF16)
+
+
+def test_decode_fused_append_tinyllama_at_scale(gpu):
+    w = W.tinyllama_decode(seed=2)
+    t = W.materialize(w, gpu)
+    before = O.to_bits(t.pool)
+    ws = workspace(gpu)
+    dw = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    dw.plan(t.kv_indptr, t.kv_indices, t.kv_last_page_len, w.hq, w.hkv, w.d, 16,
+            q_data_type=t.q.dtype)
+    out = dw.run(t.q, t.pool, append_key=t.k_new, append_value=t.v_new)
+    torch.cuda.synchronize()
+    m = w.meta
+    want, _ = O.append_pages(before, O.to_bits(t.k_new), O.to_bits(t.v_new), m.batch_indices,
+                             m.positions, m.kv_indices, m.kv_indptr)
+    assert np.array_equal(O.to_bits(t.pool), want)
+    ref_o, _ = oracle_decode(m, t.pool, t.q)
+    assert max_err(out, ref_o) <= TOL_BF16
