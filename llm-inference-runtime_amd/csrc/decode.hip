@@ -21,8 +21,8 @@
 // absent pages (num_records = 0) and slots past last_page_len read as zero
 // without touching HBM, so the loop issues a fixed number of loads per pair
 // and the compiler keeps the next pair's loads in flight while the current
-// one is computed (two register stages, ping-pong).  Page ids are scalar
-// loads issued two pairs ahead of their use.
+// one is computed (two register buffers of 16 KiB each, ping-pong).  Page
+// ids are scalar loads issued one buffer ahead of their use.
 //
 // K rows are read as 16-byte (bf16/fp16) or 8-byte (e4m3) pieces in the
 // MFMA A-operand layout (lane -> token row, 8 consecutive d).  V rows are
@@ -167,6 +167,8 @@ struct DecodeTraits {
   static constexpr int KB = 8 * ESZ;         // K bytes per lane per k-step
   static constexpr int VB = W * ESZ;         // V bytes per lane per token
   static constexpr int PAGE_BYTES = kPage * D * ESZ;
+  // page pairs per register buffer: 16 KiB of K/V per buffer
+  static constexpr int NP = (kPage * D * ESZ * 2 * 2 >= 16384) ? 1 : 2;
   using KRaw = typename RawT<KB>::type;
   using VRaw = typename RawT<VB>::type;
 };
@@ -241,11 +243,20 @@ struct SoftmaxState {
   float m, l;
 };
 
+// The new-token row of the fused append lives in the wave's own LDS slot as
+// the bits stored in the pool (e4m3 pools: quantised with the page's scale):
+// K row at byte 0, V row at byte D * ESZ.  Only the pair holding the new
+// token reads it, so it costs no registers in the main loop.
+// patch_pi >= 0: page half patch_pi of this pair holds the token appended in
+// this launch at `slot`; its stale loaded values are replaced by the new row
+// with per-lane selects where they are used.
 template <int D, bool BF16, bool FP8>
-__device__ __forceinline__ void compute_pair(Stage<D, BF16, FP8>& st,
+__device__ __forceinline__ void compute_pair(const Stage<D, BF16, FP8>& st,
                                              const u32x4 (&qf)[D / 32],
                                              SoftmaxState<D, BF16, FP8>& sm,
-                                             float scale_log2, int G) {
+                                             float scale_log2, int G, int n,
+                                             const uint8_t* new_row,
+                                             int patch_pi, int slot) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
   // ---- S^T = K . Q^T for both pages
@@ -255,11 +266,17 @@ __device__ __forceinline__ void compute_pair(Stage<D, BF16, FP8>& st,
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < Tr::KS; ++ks) {
+      typename Tr::KRaw kr = st.k[pi][ks];
+      if (patch_pi == pi) {
+        const auto nk = *reinterpret_cast<const typename Tr::KRaw*>(
+            new_row + (32 * ks + 8 * G) * Tr::ESZ);
+        if (n == slot) kr = nk;
+      }
       u32x4 a;
       if constexpr (FP8) {
-        a = e4m3x8_to_16<BF16>(st.k[pi][ks][0], st.k[pi][ks][1]);
+        a = e4m3x8_to_16<BF16>(kr[0], kr[1]);
       } else {
-        a = st.k[pi][ks];
+        a = kr;
       }
       acc = mfma16<BF16>(a, qf[ks], acc);
     }
@@ -309,20 +326,26 @@ __device__ __forceinline__ void compute_pair(Stage<D, BF16, FP8>& st,
   uint32_t vw[8][W / 2];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
+    typename Tr::VRaw vr = st.v[j];
+    if (patch_pi == (j >> 2)) {
+      const auto nv = *reinterpret_cast<const typename Tr::VRaw*>(
+          new_row + (D + W * n) * Tr::ESZ);
+      if (G == (slot >> 2) && (j & 3) == (slot & 3)) vr = nv;
+    }
     if constexpr (FP8) {
       if constexpr (W == 8) {
-        const u32x4 c = e4m3x8_to_16<BF16>(dword_of(st.v[j], 0),
-                                           dword_of(st.v[j], 1));
+        const u32x4 c = e4m3x8_to_16<BF16>(dword_of(vr, 0),
+                                           dword_of(vr, 1));
 #pragma unroll
         for (int i = 0; i < 4; ++i) vw[j][i] = c[i];
       } else {
-        const u32x2 c = e4m3x4_to_16<BF16>(dword_of(st.v[j], 0));
+        const u32x2 c = e4m3x4_to_16<BF16>(dword_of(vr, 0));
         vw[j][0] = c[0];
         vw[j][1] = c[1];
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < W / 2; ++i) vw[j][i] = dword_of(st.v[j], i);
+      for (int i = 0; i < W / 2; ++i) vw[j][i] = dword_of(vr, i);
     }
   }
   // ---- O^T += V^T . P^T, one MFMA per d offset e (tile rows d = W m + e)
@@ -338,28 +361,6 @@ __device__ __forceinline__ void compute_pair(Stage<D, BF16, FP8>& st,
     }
     sm.o[e] = mfma16<BF16>(a, pb, sm.o[e]);
   }
-}
-
-// New-token row of the fused append, held in the lanes that own it in the
-// stage layouts: K lanes with n == slot hold d = 32 ks + 8 G; V lanes with
-// G == slot / 4 hold d in [W n, W n + W).  Values are the bits stored in the
-// pool (e4m3 pools: quantised with the page's scale).
-template <int D, bool BF16, bool FP8>
-struct NewRow {
-  using Tr = DecodeTraits<D, BF16, FP8>;
-  typename Tr::KRaw k[Tr::KS];
-  typename Tr::VRaw v;
-};
-
-template <int N>
-__device__ __forceinline__ typename RawT<N>::type load_raw16(const uint16_t* src);
-template <>
-__device__ __forceinline__ u32x4 load_raw16<16>(const uint16_t* src) {
-  return *reinterpret_cast<const u32x4*>(src);
-}
-template <>
-__device__ __forceinline__ u32x2 load_raw16<8>(const uint16_t* src) {
-  return *reinterpret_cast<const u32x2*>(src);
 }
 
 // 8 sixteen-bit values -> 8 e4m3 bytes, round(clamp(x / scale, +-448)).
@@ -378,92 +379,49 @@ __device__ __forceinline__ u32x2 quant8(u32x4 x, float scale) {
   o[1] = f32_to_e4m3x4(f[4], f[5], f[6], f[7]);
   return o;
 }
-template <bool BF16>
-__device__ __forceinline__ uint32_t quant4(u32x2 x, float scale) {
-  float f[4];
-#pragma unroll
-  for (int e = 0; e < 2; ++e) {
-    f[2 * e] = h2f<BF16>((uint16_t)(x[e] & 0xffffu));
-    f[2 * e + 1] = h2f<BF16>((uint16_t)(x[e] >> 16));
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) f[e] = fminf(fmaxf(f[e] / scale, -448.f), 448.f);
-  return f32_to_e4m3x4(f[0], f[1], f[2], f[3]);
-}
-
-// Loads sequence b / head h's new row into the owning lanes and writes it to
-// slot `slot` of page `page` (the append of flashinfer.append_paged_kv_cache
-// at position kv_len - 1).
+// Writes sequence b / head h's new row to slot `slot` of page `page` (the
+// append of flashinfer.append_paged_kv_cache at position kv_len - 1) and to
+// the wave's LDS slot `new_row`.  Lanes [0, D/8) move the K row, lanes
+// [32, 32 + D/8) the V row, 8 elements each.
 template <int D, bool BF16, bool FP8>
 __device__ __forceinline__ void fused_append(const DecodeParams& p,
-                                             NewRow<D, BF16, FP8>& nr, int b,
-                                             int h, int page, int slot, int n,
-                                             int G) {
+                                             uint8_t* new_row, int b, int h,
+                                             int page, int slot, int lane) {
   using Tr = DecodeTraits<D, BF16, FP8>;
-  constexpr int W = Tr::W;
-  const uint16_t* krow = p.k_new + (int64_t)b * p.k_sn + (int64_t)h * p.k_sh;
-  const uint16_t* vrow = p.v_new + (int64_t)b * p.v_sn + (int64_t)h * p.v_sh;
-  uint8_t* kdst = const_cast<uint8_t*>(p.cache) +
-                  ((int64_t)page * 2 * p.hkv + h) * (int64_t)Tr::PAGE_BYTES +
-                  (int64_t)slot * D * Tr::ESZ;
-  uint8_t* vdst = kdst + (int64_t)p.hkv * Tr::PAGE_BYTES;
-  float ks_ = 1.f, vs_ = 1.f;
+  const int is_v = lane >> 5;
+  const int c = lane & 31;
+  if (c >= D / 8) return;
+  const uint16_t* src =
+      is_v ? p.v_new + (int64_t)b * p.v_sn + (int64_t)h * p.v_sh
+           : p.k_new + (int64_t)b * p.k_sn + (int64_t)h * p.k_sh;
+  uint8_t* dst = const_cast<uint8_t*>(p.cache) +
+                 (((int64_t)page * 2 + is_v) * p.hkv + h) * (int64_t)Tr::PAGE_BYTES +
+                 ((int64_t)slot * D + 8 * c) * Tr::ESZ;
+  uint8_t* lds = new_row + (is_v * D + 8 * c) * Tr::ESZ;
+  const u32x4 x = *reinterpret_cast<const u32x4*>(src + 8 * c);
   if constexpr (FP8) {
-    const int64_t si = ((int64_t)page * 2) * p.hkv + h;
-    ks_ = load_invariant(p.kv_scales + si);
-    vs_ = load_invariant(p.kv_scales + si + p.hkv);
-  }
-#pragma unroll
-  for (int kk = 0; kk < Tr::KS; ++kk) {
-    const u32x4 x = *reinterpret_cast<const u32x4*>(krow + 32 * kk + 8 * G);
-    if constexpr (FP8) {
-      nr.k[kk] = quant8<BF16>(x, ks_);
-    } else {
-      nr.k[kk] = x;
-    }
-    if (n == slot)
-      *reinterpret_cast<typename Tr::KRaw*>(kdst + (32 * kk + 8 * G) * Tr::ESZ) = nr.k[kk];
-  }
-  const auto vx = load_raw16<W * 2>(vrow + W * n);
-  if constexpr (FP8) {
-    if constexpr (W == 8) {
-      nr.v = quant8<BF16>(vx, vs_);
-    } else {
-      nr.v = quant4<BF16>(vx, vs_);
-    }
+    const float scale =
+        load_invariant(p.kv_scales + ((int64_t)page * 2 + is_v) * p.hkv + h);
+    const u32x2 q = quant8<BF16>(x, scale);
+    *reinterpret_cast<u32x2*>(dst) = q;
+    *reinterpret_cast<u32x2*>(lds) = q;
   } else {
-    nr.v = vx;
-  }
-  if (G == (slot >> 2))
-    *reinterpret_cast<typename Tr::VRaw*>(vdst + W * n * Tr::ESZ) = nr.v;
-}
-
-// Replace the stale slot of the new token in a loaded stage (page half pi).
-template <int D, bool BF16, bool FP8>
-__device__ __forceinline__ void patch_stage(Stage<D, BF16, FP8>& st,
-                                            const NewRow<D, BF16, FP8>& nr,
-                                            int pi, int slot, int n, int G) {
-  using Tr = DecodeTraits<D, BF16, FP8>;
-#pragma unroll
-  for (int pj = 0; pj < 2; ++pj) {
-    if (pj != pi) continue;
-#pragma unroll
-    for (int kk = 0; kk < Tr::KS; ++kk)
-      if (n == slot) st.k[pj][kk] = nr.k[kk];
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-      if (G == (slot >> 2) && r == (slot & 3)) st.v[4 * pj + r] = nr.v;
+    *reinterpret_cast<u32x4*>(dst) = x;
+    *reinterpret_cast<u32x4*>(lds) = x;
   }
 }
 
 template <int D, bool BF16, bool FP8, bool APPEND>
-__global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
+__global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
+  __shared__ __attribute__((aligned(16)))
+  uint8_t sm_new[4][APPEND ? 2 * D * DecodeTraits<D, BF16, FP8>::ESZ : 16];
   const int lane = threadIdx.x & 63;
   // wave-uniform by construction; readfirstlane tells the compiler, so item
   // fields are scalar loads and buffer descriptors stay in SGPRs
   const int wave = uniform(threadIdx.x >> 6);
+  uint8_t* new_row = sm_new[wave];
   const int gw = uniform((int)blockIdx.x * 4 + wave);
   if (gw >= p.n_waves) return;
   const int n = lane & 15;
@@ -505,7 +463,6 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
     }
 
     // the item that holds the sequence's last page also performs the append
-    NewRow<D, BF16, FP8> nr;
     int new_pg = -1;  // page index (within the sequence) of the new token
     const int new_slot = last - 1;
     if constexpr (APPEND) {
@@ -513,7 +470,7 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
         const int page = page_id(p, ind_lo, npages - 1, npages);
         if (page >= 0) {
           new_pg = npages - 1;
-          fused_append(p, nr, b, h, page, new_slot, n, G);
+          fused_append<D, BF16, FP8>(p, new_row, b, h, page, new_slot, lane);
         }
       }
     }
@@ -524,29 +481,49 @@ __global__ void __launch_bounds__(256, 2) decode_kernel(DecodeParams p) {
     sm.m = -INFINITY;
     sm.l = 0.f;
 
-    // two register stages (ping-pong); page ids run two pairs ahead
+    // Two register buffers (ping-pong) of NP page pairs each; page ids run
+    // one buffer ahead of the loads.  NP = 2 for the 8-KiB pairs (D = 64
+    // bf16/fp16, D = 128 e4m3) keeps 16 KiB per wave in flight.
+    constexpr int NP = DecodeTraits<D, BF16, FP8>::NP;
     const int n_pairs = page_hi > page_lo ? (page_hi - page_lo + 1) >> 1 : 0;
-    if (n_pairs > 0) {
-      Stage<D, BF16, FP8> sa, sb;
-      PairIds id_b = fetch_ids(p, ind_lo, page_lo + 2, page_hi);
-      load_pair(sa, p, h, fetch_ids(p, ind_lo, page_lo, page_hi), page_lo,
-                npages, last, n, G);
-      for (int i = 0; i < n_pairs; i += 2) {
-        const PairIds id_a = fetch_ids(p, ind_lo, page_lo + 2 * (i + 2), page_hi);
-        load_pair(sb, p, h, id_b, page_lo + 2 * (i + 1), npages, last, n, G);
+    const int n_chunks = (n_pairs + NP - 1) / NP;
+    auto fetch_chunk = [&](PairIds (&ids)[NP], int c) {
+#pragma unroll
+      for (int k = 0; k < NP; ++k)
+        ids[k] = fetch_ids(p, ind_lo, page_lo + 2 * (NP * c + k), page_hi);
+    };
+    auto load_chunk = [&](Stage<D, BF16, FP8> (&st)[NP], const PairIds (&ids)[NP], int c) {
+#pragma unroll
+      for (int k = 0; k < NP; ++k)
+        load_pair(st[k], p, h, ids[k], page_lo + 2 * (NP * c + k), npages, last, n, G);
+    };
+    auto compute_chunk = [&](Stage<D, BF16, FP8> (&st)[NP], int c) {
+#pragma unroll
+      for (int k = 0; k < NP; ++k) {
+        const int pr = NP * c + k;
+        if (pr >= n_pairs) break;
+        int patch_pi = -1;
         if constexpr (APPEND) {
-          const int d_pg = new_pg - (page_lo + 2 * i);
-          if (new_pg >= 0 && d_pg >= 0 && d_pg < 2) patch_stage(sa, nr, d_pg, new_slot, n, G);
+          const int d_pg = new_pg - (page_lo + 2 * pr);
+          if (new_pg >= 0 && d_pg >= 0 && d_pg < 2) patch_pi = d_pg;
         }
-        compute_pair(sa, qf, sm, p.scale_log2, G);
-        if (i + 1 >= n_pairs) break;
-        id_b = fetch_ids(p, ind_lo, page_lo + 2 * (i + 3), page_hi);
-        load_pair(sa, p, h, id_a, page_lo + 2 * (i + 2), npages, last, n, G);
-        if constexpr (APPEND) {
-          const int d_pg = new_pg - (page_lo + 2 * (i + 1));
-          if (new_pg >= 0 && d_pg >= 0 && d_pg < 2) patch_stage(sb, nr, d_pg, new_slot, n, G);
-        }
-        compute_pair(sb, qf, sm, p.scale_log2, G);
+        compute_pair(st[k], qf, sm, p.scale_log2, G, n, new_row, patch_pi, new_slot);
+      }
+    };
+    if (n_chunks > 0) {
+      Stage<D, BF16, FP8> sa[NP], sb[NP];
+      PairIds ida[NP], idb[NP];
+      fetch_chunk(ida, 0);
+      fetch_chunk(idb, 1);
+      load_chunk(sa, ida, 0);
+      for (int c = 0; c < n_chunks; c += 2) {
+        fetch_chunk(ida, c + 2);
+        load_chunk(sb, idb, c + 1);
+        compute_chunk(sa, c);
+        if (c + 1 >= n_chunks) break;
+        fetch_chunk(idb, c + 3);
+        load_chunk(sa, ida, c + 2);
+        compute_chunk(sb, c + 1);
       }
     }
 
