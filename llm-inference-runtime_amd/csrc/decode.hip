@@ -43,8 +43,9 @@ namespace pa {
 
 struct DecodeParams {
   const DecodeItem* items;
-  const int32_t* wave_ptr;  // [n_waves + 1]: items of wave w
-  int32_t n_waves, n_merge, n_slots, batch_size;
+  const int32_t* wave_ptr;  // [n_groups + 1]: items of head group w
+  int32_t n_groups, n_merge, n_slots, batch_size;
+  int32_t hg_shift;  // log2(waves per head group), 0..2
   const uint16_t* q;
   int64_t q_sn, q_sh;
   const uint8_t* cache;
@@ -422,8 +423,12 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
   // fields are scalar loads and buffer descriptors stay in SGPRs
   const int wave = uniform(threadIdx.x >> 6);
   uint8_t* new_row = sm_new[wave];
-  const int gw = uniform((int)blockIdx.x * 4 + wave);
-  if (gw >= p.n_waves) return;
+  // head group gw = the hg consecutive waves of a workgroup; wave wi of the
+  // group takes KV head h0 + wi of every item, so the group reads each page's
+  // K (then V) blocks of hg heads, one contiguous run, at the same time
+  const int wi = wave & ((1 << p.hg_shift) - 1);
+  const int gw = uniform(((int)blockIdx.x * 4 + wave) >> p.hg_shift);
+  if (gw >= p.n_groups) return;
   const int n = lane & 15;
   const int G = lane >> 4;
   const int g = p.g;
@@ -433,13 +438,15 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
   for (int it = it_lo; it < it_hi; ++it) {
     const int32_t* itp = reinterpret_cast<const int32_t*>(p.items + it);
     const int b = uniform(load_invariant(itp + 0));
-    const int h = uniform(load_invariant(itp + 1));
+    const int h0 = uniform(load_invariant(itp + 1));
     const int item_lo = uniform(load_invariant(itp + 2));
     const int item_hi = uniform(load_invariant(itp + 3));
-    const int slot = uniform(load_invariant(itp + 4));
+    const int slot0 = uniform(load_invariant(itp + 4));
     const int merge = uniform(load_invariant(itp + 5));
+    const int h = h0 + wi;
+    const int slot = slot0 >= 0 ? slot0 + wi : -1;
     // a work list that does not match this launch is skipped, never followed
-    if (b < 0 || b >= p.batch_size || h < 0 || h >= p.hkv ||
+    if (b < 0 || b >= p.batch_size || h0 < 0 || h >= p.hkv ||
         slot >= p.n_slots || merge >= p.n_merge || (slot >= 0) != (merge >= 0))
       continue;
     const int ind_lo = uniform(load_invariant(p.kv_indptr + b));
@@ -584,12 +591,12 @@ __global__ void __launch_bounds__(128)
   const int head = mi.h * g + hn;
   float M = -INFINITY;
   for (int s = 0; s < mi.nslots; ++s)
-    M = fmaxf(M, pl[(int64_t)(mi.slot0 + s) * g + hn]);
+    M = fmaxf(M, pl[(int64_t)(mi.slot0 + s * mi.stride) * g + hn]);
   float num = 0.f, den = 0.f;
   const int dd = threadIdx.x;
   if (M != -INFINITY) {
     for (int s = 0; s < mi.nslots; ++s) {
-      const int64_t sh = (int64_t)(mi.slot0 + s) * g + hn;
+      const int64_t sh = (int64_t)(mi.slot0 + s * mi.stride) * g + hn;
       const float wt = exp2f(pl[sh] - M);
       den += wt;
       if (dd < d) num += wt * po[sh * d + dd];
@@ -632,6 +639,20 @@ static int decode_waves_per_cu() {
   return 4;
 }
 
+// Waves (KV heads) per head group: the largest of 4, 2, 1 that divides Hkv,
+// so a page's K and V blocks are each read as one run of hg * 16 rows;
+// PAGEDATTN_DECODE_HEAD_GROUP (1, 2 or 4) caps it.
+static int decode_head_group(int hkv) {
+  int cap = 4;
+  if (const char* env = std::getenv("PAGEDATTN_DECODE_HEAD_GROUP")) {
+    const int v = std::atoi(env);
+    if (v == 1 || v == 2 || v == 4) cap = v;
+  }
+  int hg = 1;
+  while (hg * 2 <= cap && hkv % (hg * 2) == 0) hg *= 2;
+  return hg;
+}
+
 }  // namespace pa
 
 using namespace pa;
@@ -672,37 +693,42 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   }
   int cus = device_cu_count();
   if (cus <= 0) cus = 256;
-  const int64_t waves_max = std::max<int64_t>(1, (int64_t)cus * decode_waves_per_cu());
+  // work is planned per head group: hg KV heads walked together by hg waves
+  const int hg = decode_head_group(hkv);
+  const int hg_shift = hg == 4 ? 2 : hg == 2 ? 1 : 0;
+  const int ngrp = hkv / hg;  // head groups per sequence
+  const int64_t groups_max =
+      std::max<int64_t>(1, (int64_t)cus * decode_waves_per_cu() / hg);
 
-  // items, grouped per wave
+  // items, grouped per head group
   std::vector<DecodeItem> items;
   std::vector<int32_t> wave_ptr(1, 0);
-  std::vector<int32_t> pieces((size_t)batch_size * hkv, 0);
-  auto make = [](int b, int h, int lo, int hi) {
-    return DecodeItem{b, h, lo, hi, -1, -1, 0, 0};
+  std::vector<int32_t> pieces((size_t)batch_size * ngrp, 0);
+  auto make = [hg](int b, int hgrp, int lo, int hi) {
+    return DecodeItem{b, hgrp * hg, lo, hi, -1, -1, 0, 0};
   };
   if (split_pages != 0) {
-    // fixed chunks (split_pages > 0) or whole sequences (< 0), assigned to
-    // waves longest-first onto the least-loaded wave
+    // fixed chunks (split_pages > 0) or whole sequences (< 0), assigned
+    // longest-first onto the least-loaded head group
     const int chunk = split_pages > 0 ? ((split_pages + 7) / 8) * 8 : INT32_MAX;
     std::vector<DecodeItem> all;
     for (int b = 0; b < batch_size; ++b)
-      for (int h = 0; h < hkv; ++h) {
+      for (int hgrp = 0; hgrp < ngrp; ++hgrp) {
         if (npages[b] == 0) {
-          all.push_back(make(b, h, 0, 0));
-          pieces[(size_t)b * hkv + h]++;
+          all.push_back(make(b, hgrp, 0, 0));
+          pieces[(size_t)b * ngrp + hgrp]++;
           continue;
         }
         for (int lo = 0; lo < npages[b]; lo += chunk) {
-          all.push_back(make(b, h, lo, (int)std::min<int64_t>(npages[b], (int64_t)lo + chunk)));
-          pieces[(size_t)b * hkv + h]++;
+          all.push_back(make(b, hgrp, lo, (int)std::min<int64_t>(npages[b], (int64_t)lo + chunk)));
+          pieces[(size_t)b * ngrp + hgrp]++;
         }
       }
     std::stable_sort(all.begin(), all.end(), [](const DecodeItem& a, const DecodeItem& c) {
       return a.page_hi - a.page_lo > c.page_hi - c.page_lo;
     });
-    const int64_t nw = std::min<int64_t>(waves_max, std::max<size_t>(1, all.size()));
-    std::vector<std::vector<int>> per_wave(nw);
+    const int64_t nw = std::min<int64_t>(groups_max, std::max<size_t>(1, all.size()));
+    std::vector<std::vector<int>> per_group(nw);
     std::priority_queue<std::pair<int64_t, int64_t>,
                         std::vector<std::pair<int64_t, int64_t>>,
                         std::greater<std::pair<int64_t, int64_t>>> heap;
@@ -710,31 +736,31 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
     for (size_t i = 0; i < all.size(); ++i) {
       auto top = heap.top();
       heap.pop();
-      per_wave[top.second].push_back((int)i);
+      per_group[top.second].push_back((int)i);
       top.first += std::max(1, all[i].page_hi - all[i].page_lo);
       heap.push(top);
     }
-    for (auto& lst : per_wave) {
+    for (auto& lst : per_group) {
       for (int i : lst) items.push_back(all[i]);
       wave_ptr.push_back((int32_t)items.size());
     }
   } else {
-    // balanced: the (sequence, head, page) stream cut into equal shares
-    int64_t target = (total * hkv + waves_max - 1) / waves_max;
+    // balanced: the (sequence, head group, page) stream cut into equal shares
+    int64_t target = (total * ngrp + groups_max - 1) / groups_max;
     target = std::max<int64_t>(4, (target + 1) / 2 * 2);
     int64_t fill = 0;
     for (int b = 0; b < batch_size; ++b)
-      for (int h = 0; h < hkv; ++h) {
+      for (int hgrp = 0; hgrp < ngrp; ++hgrp) {
         if (npages[b] == 0) {
-          items.push_back(make(b, h, 0, 0));
-          pieces[(size_t)b * hkv + h]++;
+          items.push_back(make(b, hgrp, 0, 0));
+          pieces[(size_t)b * ngrp + hgrp]++;
           continue;
         }
         int lo = 0;
         while (lo < npages[b]) {
           const int take = (int)std::min<int64_t>(npages[b] - lo, target - fill);
-          items.push_back(make(b, h, lo, lo + take));
-          pieces[(size_t)b * hkv + h]++;
+          items.push_back(make(b, hgrp, lo, lo + take));
+          pieces[(size_t)b * ngrp + hgrp]++;
           lo += take;
           fill += take;
           if (fill == target) {
@@ -747,26 +773,31 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
       wave_ptr.push_back((int32_t)items.size());
   }
 
-  // partial slots and merge groups for (sequence, head) pairs cut in pieces
+  // Partial slots and merge groups for (sequence, head group) pairs cut in
+  // pieces: piece k of head h0 + i writes slot base + k * hg + i, and the
+  // merge of (b, h0 + i) reads slots base + i + k * hg.
   std::vector<MergeItem> merges;
-  std::vector<int32_t> group_of((size_t)batch_size * hkv, -1);
+  std::vector<int32_t> first_merge((size_t)batch_size * ngrp, -1);
+  std::vector<int32_t> base_slot((size_t)batch_size * ngrp, -1);
   int n_slots = 0;
   for (int b = 0; b < batch_size; ++b)
-    for (int h = 0; h < hkv; ++h) {
-      const int np = pieces[(size_t)b * hkv + h];
+    for (int hgrp = 0; hgrp < ngrp; ++hgrp) {
+      const int np = pieces[(size_t)b * ngrp + hgrp];
       if (np > 1) {
-        group_of[(size_t)b * hkv + h] = (int)merges.size();
-        merges.push_back(MergeItem{b, h, n_slots, np});
-        n_slots += np;
+        first_merge[(size_t)b * ngrp + hgrp] = (int)merges.size();
+        base_slot[(size_t)b * ngrp + hgrp] = n_slots;
+        for (int i = 0; i < hg; ++i)
+          merges.push_back(MergeItem{b, hgrp * hg + i, n_slots + i, np, hg});
+        n_slots += np * hg;
       }
     }
   {
-    std::vector<int32_t> next(merges.size(), 0);
+    std::vector<int32_t> next((size_t)batch_size * ngrp, 0);
     for (auto& it : items) {
-      const int grp = group_of[(size_t)it.b * hkv + it.h];
-      if (grp >= 0) {
-        it.merge = grp;
-        it.slot = merges[grp].slot0 + next[grp]++;
+      const size_t key = (size_t)it.b * ngrp + it.h / hg;
+      if (first_merge[key] >= 0) {
+        it.merge = first_merge[key];
+        it.slot = base_slot[key] + hg * next[key]++;
       }
     }
   }
@@ -803,6 +834,7 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   plan->d = head_dim;
   plan->page_size = page_size;
   plan->n_items = n_waves;
+  plan->hg_shift = hg_shift;
   plan->n_merge = (int)n_merge;
   plan->n_slots = n_slots;
   plan->split_pages = split_pages;
@@ -868,7 +900,8 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   DecodeParams p;
   p.items = static_cast<const DecodeItem*>(plan->items_dev);
   p.wave_ptr = plan->wave_ptr_dev;
-  p.n_waves = plan->n_items;
+  p.n_groups = plan->n_items;
+  p.hg_shift = plan->hg_shift;
   p.n_merge = plan->n_merge;
   p.n_slots = plan->n_slots;
   p.batch_size = plan->batch_size;
@@ -900,7 +933,7 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = q_dtype == PAGEDATTN_BF16;
   DecodeFn fn = pick_decode(plan->d, bf16, fp8, app != nullptr);
-  const int blocks = (plan->n_items + 3) / 4;
+  const int blocks = ((plan->n_items << plan->hg_shift) + 3) / 4;
   hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, s, p);
   int rc = check_launch(who);
   if (rc || plan->n_merge == 0) return rc;

@@ -15,18 +15,19 @@ namespace pa {
 
 enum PlanMode { kPlanNone = 0, kPlanDecode = 1, kPlanPrefill = 2 };
 
-// One decode work item, processed by one wave: pages [page_lo, page_hi) of
-// sequence b for KV head h and all its query heads.  slot < 0 means the item
-// covers the whole sequence and writes the final output; otherwise it writes
-// split partials to `slot` and takes part in merge group `merge`.
+// One decode work item, processed by one head group of hg waves: pages
+// [page_lo, page_hi) of sequence b for KV heads [h, h + hg), one wave per KV
+// head and all its query heads.  slot < 0 means the item covers the whole
+// sequence and writes the final output; otherwise wave i writes split
+// partials to `slot + i` and the item takes part in merge group `merge`.
 struct DecodeItem {
   int32_t b, h, page_lo, page_hi, slot, merge, pad0, pad1;
 };
 
-// Split-KV merge group: (sequence b, KV head h) owns partial slots
-// [slot0, slot0 + nslots).
+// Split-KV merge group: (sequence b, KV head h) owns the partial slots
+// slot0 + k * stride, k in [0, nslots).
 struct MergeItem {
-  int32_t b, h, slot0, nslots;
+  int32_t b, h, slot0, nslots, stride;
 };
 
 // One prefill work item: query tokens [q_lo, q_hi) of sequence b (relative to
@@ -48,14 +49,16 @@ inline size_t ws_align(size_t x) { return (x + kWsAlign - 1) & ~(kWsAlign - 1); 
 struct pagedattn_plan {
   int mode = pa::kPlanNone;
   int batch_size = 0, hq = 0, hkv = 0, d = 0, page_size = 0;
-  // decode: n_items = waves (decode) or work items (prefill)
+  // n_items = head groups (decode) or work items (prefill)
   int n_items = 0, n_merge = 0, n_slots = 0, split_pages = 0;
+  // decode: log2 of the waves (KV heads) per head group
+  int hg_shift = 0;
   // prefill: query tokens per tile (rows = tokens * hq/hkv)
   int q_tile = 0;
   int64_t total_qo = 0;
   // device pointers into the workspace
   void* items_dev = nullptr;
-  const int32_t* wave_ptr_dev = nullptr;  // decode: items of wave w
+  const int32_t* wave_ptr_dev = nullptr;  // decode: items of head group w
   void* merge_dev = nullptr;
   float* partial_o = nullptr;
   float* partial_lse = nullptr;

@@ -37,6 +37,20 @@ def test_decode_edge_lengths(gpu, d, hq, hkv):
         assert lse_err(lse, ref_l) <= TOL_LSE, split
 
 
+@pytest.mark.parametrize("head_group", ["1", "2", "4"])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (16, 2)])
+def test_decode_head_groups(gpu, monkeypatch, head_group, hq, hkv):
+    # every head-group width (waves walking the same pages, one per KV head)
+    # gives the oracle's answer, whole-sequence, balanced and fixed splits
+    monkeypatch.setenv("PAGEDATTN_DECODE_HEAD_GROUP", head_group)
+    meta, pool, q = decode_case(gpu, EDGE_LENS, hq, hkv, 64, seed=5 + hkv)
+    ref_o, ref_l = oracle_decode(meta, pool, q)
+    for split in (-1, 0, 8):
+        out, lse = run_decode(gpu, meta, pool, q, hq, hkv, 64, split_pages=split)
+        assert max_err(out, ref_o) <= TOL_BF16, (split, max_err(out, ref_o))
+        assert lse_err(lse, ref_l) <= TOL_LSE, split
+
+
 def test_decode_fp16(gpu):
     meta, pool, q = decode_case(gpu, EDGE_LENS, 32, 4, 64, dtype=torch.float16, seed=11)
     ref_o, ref_l = oracle_decode(meta, pool, q)
