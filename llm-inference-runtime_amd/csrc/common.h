@@ -105,6 +105,20 @@ __device__ __forceinline__ uint16_t f2h(float f) {
   }
 }
 
+// Two floats -> two 16-bit values in one dword (element a low), round to
+// nearest even: one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <bool IS_BF16>
+__device__ __forceinline__ uint32_t pack2_16(float a, float b) {
+  const f32x2 v = {a, b};
+  if constexpr (IS_BF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  } else {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  }
+}
+
 // fp32 -> fp8 e4m3fn (OCP, the gfx950 fp8 format) through the hardware
 // converter, round to nearest even.  It saturates nothing by itself: callers
 // clamp to +-448 first.

@@ -34,6 +34,7 @@ namespace pa {
 
 struct PrefillParams {
   const PrefillItem* items;
+  int32_t n_items, batch_size;
   const uint16_t* q;
   int64_t q_sn, q_sh;
   const int32_t* qo_indptr;
@@ -76,11 +77,6 @@ __device__ __forceinline__ uint32_t e4m3x2_to16(uint32_t w) {
   }
 }
 
-template <bool BF16>
-__device__ __forceinline__ uint32_t pack2h(float a, float b) {
-  return (uint32_t)f2h<BF16>(a) | ((uint32_t)f2h<BF16>(b) << 16);
-}
-
 template <int D, bool BF16, bool FP8, int RB>
 struct PrefillCfg {
   static constexpr int ESZ = FP8 ? 1 : 2;
@@ -105,35 +101,42 @@ struct TileRegs {
   using C = PrefillCfg<D, BF16, FP8, RB>;
   typename C::Raw k[C::CPT];
   typename C::Raw v[C::CPT];
+  float sc;  // e4m3 pools: lanes 0-3 the K scales, 4-7 the V scales of the tile's pages
 };
 
 // Issue the global loads of K/V tile `tile` (always the same number of loads:
-// missing pages are zero-sized buffers).
+// missing pages are zero-sized buffers).  Page ids are scalar loads.
 template <int D, bool BF16, bool FP8, int RB>
 __device__ __forceinline__ void load_tile(TileRegs<D, BF16, FP8, RB>& tr,
                                           const PrefillParams& p, int h,
                                           int ind_lo, int npages, int last,
-                                          int tile) {
+                                          int tile, int wave, int lane) {
   using C = PrefillCfg<D, BF16, FP8, RB>;
+  int page[4], ntok[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int pg = tile * 4 + j;
+    int id = -1;
+    if (pg < npages && ind_lo >= 0 && ind_lo + pg < p.num_indices) {
+      id = uniform(load_invariant(p.kv_indices + ind_lo + pg));
+      if (id >= p.num_pages) id = -1;
+    }
+    page[j] = id < 0 ? 0 : id;
+    ntok[j] = id < 0 ? 0 : (pg == npages - 1 ? last : kPage);
+  }
 #pragma unroll
   for (int k = 0; k < C::CPT; ++k) {
-    const int c = threadIdx.x + 256 * k;
+    const int c = lane + 64 * wave + 256 * k;
     const int tok = c / (D / 8);
     const int d0 = (c % (D / 8)) * 8;
-    // the 64 chunks of a wave lie in one page
-    const int pg = uniform(tile * 4 + tok / kPage);
-    int ntok = 0, page = 0;
-    if (pg < npages && ind_lo >= 0 && ind_lo + pg < p.num_indices) {
-      page = uniform(p.kv_indices[ind_lo + pg]);
-      if (page >= 0 && page < p.num_pages)
-        ntok = pg == npages - 1 ? last : kPage;
-      else
-        page = 0;
-    }
+    // the 64 chunks of a wave lie in one page: j is wave-uniform
+    const int j = uniform((64 * wave + 256 * k) / (D / 8) / kPage);
+    const int pj = j == 0 ? page[0] : j == 1 ? page[1] : j == 2 ? page[2] : page[3];
+    const int nj = j == 0 ? ntok[0] : j == 1 ? ntok[1] : j == 2 ? ntok[2] : ntok[3];
     const uint8_t* kb =
-        p.cache + ((int64_t)page * 2 * p.hkv + h) * (int64_t)C::PAGE_BYTES;
+        p.cache + ((int64_t)pj * 2 * p.hkv + h) * (int64_t)C::PAGE_BYTES;
     const uint8_t* vb = kb + (int64_t)p.hkv * C::PAGE_BYTES;
-    const uint32_t bytes = (uint32_t)(ntok * D * C::ESZ);
+    const uint32_t bytes = (uint32_t)(nj * D * C::ESZ);
     const uint32_t off = (uint32_t)(((tok % kPage) * D + d0) * C::ESZ);
     if constexpr (FP8) {
       tr.k[k] = buf_load8(make_rsrc(kb, bytes), off);
@@ -143,15 +146,25 @@ __device__ __forceinline__ void load_tile(TileRegs<D, BF16, FP8, RB>& tr,
       tr.v[k] = buf_load16(make_rsrc(vb, bytes), off);
     }
   }
+  if constexpr (FP8) {
+    tr.sc = 0.f;
+    if (lane < 8) {
+      const int j = lane & 3;
+      const int pj = j == 0 ? page[0] : j == 1 ? page[1] : j == 2 ? page[2] : page[3];
+      const int nj = j == 0 ? ntok[0] : j == 1 ? ntok[1] : j == 2 ? ntok[2] : ntok[3];
+      if (nj > 0) tr.sc = p.kv_scales[((int64_t)pj * 2 + (lane >> 2)) * p.hkv + h];
+    }
+  }
 }
 
 template <int D, bool BF16, bool FP8, int RB>
 __device__ __forceinline__ void store_tile(const TileRegs<D, BF16, FP8, RB>& tr,
-                                           uint16_t* ks, uint16_t* vs) {
+                                           uint16_t* ks, uint16_t* vs,
+                                           int wave, int lane) {
   using C = PrefillCfg<D, BF16, FP8, RB>;
 #pragma unroll
   for (int k = 0; k < C::CPT; ++k) {
-    const int c = threadIdx.x + 256 * k;
+    const int c = lane + 64 * wave + 256 * k;
     const int tok = c / (D / 8);
     const int d0 = (c % (D / 8)) * 8;
     u32x4 kx, vx;
@@ -173,13 +186,23 @@ __device__ __forceinline__ void store_tile(const TileRegs<D, BF16, FP8, RB>& tr,
   }
 }
 
+__device__ __forceinline__ float lane_value(float v, int i) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), i));
+}
+
+// Rescale threshold (log2 units): the running max of a row is only moved
+// when a tile raises it by more than this, so P = 2^(s - m) <= 2^8 and the
+// rescale of O and l runs on few tiles.
+constexpr float kRescaleSlack = 8.f;
+
 template <int D, bool BF16, bool FP8, int RB>
 __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
   using C = PrefillCfg<D, BF16, FP8, RB>;
   constexpr int BN = C::BN;
-  __shared__ __attribute__((aligned(16))) uint16_t ks[BN * C::KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[BN * C::VSTR];
-  __shared__ float kv_sc[2][4];
+  // two K/V tile buffers: tile t + 1 is written while tile t is read
+  __shared__ __attribute__((aligned(16))) uint16_t ks[2][BN * C::KSTR];
+  __shared__ __attribute__((aligned(16))) uint16_t vs[2][BN * C::VSTR];
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -187,17 +210,20 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
   const int half = lane >> 5;  // k-half of the MFMA operands
   const int h = blockIdx.y;
   const int g = p.g;
-
-  const PrefillItem item = p.items[blockIdx.x];
-  const int b = uniform(item.b);
-  const int qo_start = uniform(p.qo_indptr[b]);
-  const int qo_len = max(0, uniform(p.qo_indptr[b + 1]) - qo_start);
-  const int q_lo = uniform(item.q_lo);
-  const int q_hi = min(uniform(item.q_hi), qo_len);
+  // a work list that does not match this launch is skipped, never followed
+  // (every condition is uniform over the workgroup)
+  if ((int)blockIdx.x >= p.n_items || h >= p.hkv) return;
+  const int32_t* itp = reinterpret_cast<const int32_t*>(p.items + blockIdx.x);
+  const int b = uniform(load_invariant(itp + 0));
+  if (b < 0 || b >= p.batch_size) return;
+  const int qo_start = uniform(load_invariant(p.qo_indptr + b));
+  const int qo_len = max(0, uniform(load_invariant(p.qo_indptr + b + 1)) - qo_start);
+  const int q_lo = max(0, uniform(load_invariant(itp + 1)));
+  const int q_hi = min(uniform(load_invariant(itp + 2)), qo_len);
   if (q_lo >= q_hi) return;
-  const int ind_lo = uniform(p.kv_indptr[b]);
-  const int npages = max(0, uniform(p.kv_indptr[b + 1]) - ind_lo);
-  const int last = min(max(uniform(p.last_page_len[b]), 1), kPage);
+  const int ind_lo = uniform(load_invariant(p.kv_indptr + b));
+  const int npages = max(0, uniform(load_invariant(p.kv_indptr + b + 1)) - ind_lo);
+  const int last = min(max(uniform(load_invariant(p.last_page_len + b)), 1), kPage);
   const int kv_len = npages > 0 ? (npages - 1) * kPage + last : 0;
   const int diag = kv_len - qo_len;  // row i sees kv j <= diag + i
   const int kv_end =
@@ -215,7 +241,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
     const int row = 32 * (RB * wave + rb) + col;
     const int qi = q_lo + row / g;
     rvalid[rb] = qi < q_hi;
-    lim[rb] = p.causal ? diag + qi : kv_len - 1;
+    lim[rb] = p.causal ? min(diag + qi, kv_len - 1) : kv_len - 1;
     const uint16_t* qp =
         p.q + (int64_t)(qo_start + (rvalid[rb] ? qi : q_lo)) * p.q_sn +
         (int64_t)(h * g + row % g) * p.q_sh + 8 * half;
@@ -238,25 +264,19 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
   }
 
   TileRegs<D, BF16, FP8, RB> tr;
-  if (n_tiles > 0) load_tile(tr, p, h, ind_lo, npages, last, 0);
+  float sc_cur = 0.f;  // e4m3 scales of the tile being computed (lanes 0-7)
+  if (n_tiles > 0) {
+    load_tile(tr, p, h, ind_lo, npages, last, 0, wave, lane);
+    store_tile(tr, ks[0], vs[0], wave, lane);
+    if constexpr (FP8) sc_cur = tr.sc;
+  }
+  __syncthreads();
+  if (n_tiles > 1) load_tile(tr, p, h, ind_lo, npages, last, 1, wave, lane);
 
   for (int t = 0; t < n_tiles; ++t) {
-    store_tile(tr, ks, vs);
-    if constexpr (FP8) {
-      if (threadIdx.x < 8) {
-        const int pg = t * 4 + (threadIdx.x & 3);
-        float sc = 0.f;
-        if (pg < npages && ind_lo + pg < p.num_indices) {
-          const int page = p.kv_indices[ind_lo + pg];
-          if (page >= 0 && page < p.num_pages)
-            sc = p.kv_scales[((int64_t)page * 2 + (threadIdx.x >> 2)) * p.hkv + h];
-        }
-        kv_sc[threadIdx.x >> 2][threadIdx.x & 3] = sc;
-      }
-    }
-    __syncthreads();
-    // next tile's loads stay in flight during this tile's math
-    if (t + 1 < n_tiles) load_tile(tr, p, h, ind_lo, npages, last, t + 1);
+    const int cur = t & 1;
+    const uint16_t* kt = ks[cur];
+    const uint16_t* vt = vs[cur];
 
     // ---- S^T = K . Q^T
     f32x16 s[RB][2];
@@ -267,52 +287,68 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
 #pragma unroll
       for (int ks_ = 0; ks_ < C::KS; ++ks_) {
         const u32x4 a = *reinterpret_cast<const u32x4*>(
-            ks + (32 * mt + col) * C::KSTR + 16 * ks_ + 8 * half);
+            kt + (32 * mt + col) * C::KSTR + 16 * ks_ + 8 * half);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) s[rb][mt] = mfma32<BF16>(a, qf[rb][ks_], s[rb][mt]);
       }
     }
 
-    // ---- online softmax; lane holds 32 of the tile's 64 tokens of its row
+    // ---- online softmax in log2 units; lane holds 32 of the tile's 64
+    // tokens of its row (token 32 mt + 8 (i/4) + 4 half + i%4 in register i)
     const int tok0 = t * BN;
     const bool need_mask = tok0 + BN > clean_end;
-    float ksc[4];
+    float ksc[4], vsc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) ksc[i] = FP8 ? kv_sc[0][i] * p.scale_log2 : p.scale_log2;
+    for (int i = 0; i < 4; ++i) {
+      ksc[i] = FP8 ? lane_value(sc_cur, i) * p.scale_log2 : p.scale_log2;
+      vsc[i] = FP8 ? lane_value(sc_cur, 4 + i) : 1.f;
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
+      if constexpr (FP8) {
+        // per-page K scales differ inside the tile: scale before the max
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) s[rb][mt][i] *= ksc[2 * mt + (i >> 3)];
+      }
+      if (need_mask) {
+        const int rel = lim[rb] - tok0 - 4 * half;  // visible iff offset <= rel
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            if (32 * mt + 8 * (i >> 2) + (i & 3) > rel) s[rb][mt][i] = -INFINITY;
+      }
       float mx = -INFINITY;
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          float v = s[rb][mt][i] * ksc[2 * mt + (i >> 3)];
-          if (need_mask) {
-            const int tok = tok0 + 32 * mt + 8 * (i >> 2) + 4 * half + (i & 3);
-            if (tok > lim[rb] || tok >= kv_len) v = -INFINITY;
-          }
-          s[rb][mt][i] = v;
-          mx = fmaxf(mx, v);
-        }
-      }
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[rb][mt][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m[rb], mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m[rb] - m_use);
+      const float c = FP8 ? 1.f : p.scale_log2;  // > 0: max commutes with it
+      const float mxs = mx * c;
+      if (__builtin_amdgcn_ballot_w64(mxs > m[rb] + kRescaleSlack)) {
+        const float m_new = fmaxf(m[rb], mxs);
+        const float alpha =
+            m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[rb] - m_new);
+        l[rb] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) o[rb][dt] *= alpha;
+        m[rb] = m_new;
+      }
+      const float mu = m[rb] == -INFINITY ? 0.f : m[rb];
       float rs = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float e = exp2f(s[rb][mt][i] - m_use);
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][mt][i], c, -mu));
           s[rb][mt][i] = e;
           rs += e;
         }
       }
-      l[rb] = l[rb] * alpha + rs;
-      m[rb] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < C::DT; ++dt) o[rb][dt] *= alpha;
+      l[rb] += rs;
     }
 
     // ---- O^T += V^T . P^T over 4 steps of 16 tokens
@@ -321,11 +357,11 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
       u32x4 pb[RB];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        const float vsc = FP8 ? kv_sc[1][st] : 1.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r0 = 8 * (st & 1) + 2 * i;
-          pb[rb][i] = pack2h<BF16>(s[rb][st >> 1][r0] * vsc, s[rb][st >> 1][r0 + 1] * vsc);
+          pb[rb][i] = pack2_16<BF16>(s[rb][st >> 1][r0] * vsc[st],
+                                     s[rb][st >> 1][r0 + 1] * vsc[st]);
         }
       }
       // transpose reads: lane (group qg, index L) points at
@@ -337,19 +373,24 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) {
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(vs + vrow * C::VSTR + 32 * dt + vcol));
+            (lds_i16x4*)(vt + vrow * C::VSTR + 32 * dt + vcol));
         const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(vs + (vrow + 8) * C::VSTR + 32 * dt + vcol));
-        u32x4 a;
-        a[0] = (uint16_t)lo[0] | ((uint32_t)(uint16_t)lo[1] << 16);
-        a[1] = (uint16_t)lo[2] | ((uint32_t)(uint16_t)lo[3] << 16);
-        a[2] = (uint16_t)hi[0] | ((uint32_t)(uint16_t)hi[1] << 16);
-        a[3] = (uint16_t)hi[2] | ((uint32_t)(uint16_t)hi[3] << 16);
+            (lds_i16x4*)(vt + (vrow + 8) * C::VSTR + 32 * dt + vcol));
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
+        const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
+        const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) o[rb][dt] = mfma32<BF16>(a, pb[rb], o[rb][dt]);
       }
     }
+
+    // ---- stage tile t + 1 into the other buffer, then fetch tile t + 2
+    if (t + 1 < n_tiles) {
+      store_tile(tr, ks[cur ^ 1], vs[cur ^ 1], wave, lane);
+      if constexpr (FP8) sc_cur = tr.sc;
+    }
     __syncthreads();
+    if (t + 2 < n_tiles) load_tile(tr, p, h, ind_lo, npages, last, t + 2, wave, lane);
   }
 
   // ---- epilogue: O^T / l, lane's row, 4 consecutive d per register quad
@@ -367,8 +408,8 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         u32x2 w;
-        w[0] = pack2h<BF16>(o[rb][dt][4 * i4] * inv, o[rb][dt][4 * i4 + 1] * inv);
-        w[1] = pack2h<BF16>(o[rb][dt][4 * i4 + 2] * inv, o[rb][dt][4 * i4 + 3] * inv);
+        w[0] = pack2_16<BF16>(o[rb][dt][4 * i4] * inv, o[rb][dt][4 * i4 + 1] * inv);
+        w[1] = pack2_16<BF16>(o[rb][dt][4 * i4 + 2] * inv, o[rb][dt][4 * i4 + 3] * inv);
         *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * half) = w;
       }
     }
@@ -503,6 +544,9 @@ int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
   if (fp8 && !kv_scales)
     return set_error(PAGEDATTN_ERR_INVALID, "%s: e4m3 pool needs kv_scales",
                      who);
+  if (!(sm_scale > 0.f) || !std::isfinite(sm_scale))
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                     "%s: sm_scale must be a positive finite number", who);
   if (plan->n_items == 0) return PAGEDATTN_OK;
   if (!q || !qo_indptr || !paged_kv_cache || !kv_indices || !kv_indptr ||
       !kv_last_page_len || !out)
@@ -517,6 +561,8 @@ int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
     return set_error(PAGEDATTN_ERR_INVALID, "%s: negative sizes", who);
   PrefillParams p;
   p.items = static_cast<const PrefillItem*>(plan->items_dev);
+  p.n_items = plan->n_items;
+  p.batch_size = plan->batch_size;
   p.q = static_cast<const uint16_t*>(q);
   p.q_sn = q_stride_n;
   p.q_sh = q_stride_h;
