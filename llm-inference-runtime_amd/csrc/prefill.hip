@@ -23,6 +23,7 @@
 // Causal tiles entirely below the diagonal skip masking; tiles above the last
 // row's diagonal are never visited.
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstring>
 #include <type_traits>
@@ -104,54 +105,85 @@ struct TileRegs {
   float sc;  // e4m3 pools: lanes 0-3 the K scales, 4-7 the V scales of the tile's pages
 };
 
-// Issue the global loads of K/V tile `tile` (always the same number of loads:
-// missing pages are zero-sized buffers).  Page ids are scalar loads.
-template <int D, bool BF16, bool FP8, int RB>
-__device__ __forceinline__ void load_tile(TileRegs<D, BF16, FP8, RB>& tr,
-                                          const PrefillParams& p, int h,
-                                          int ind_lo, int npages, int last,
-                                          int tile, int wave, int lane) {
-  using C = PrefillCfg<D, BF16, FP8, RB>;
+// Page ids of tile `tile` as a vector load: lane j < 4 gets the id of the
+// tile's page j (-1 past the sequence).  Issued one tile ahead of the K/V
+// loads that use it, it is waited on with the in-order vector counter, so
+// no K/V load ever waits for a page-id fetch.
+__device__ __forceinline__ int fetch_page_ids(const PrefillParams& p,
+                                              int ind_lo, int npages,
+                                              int tile, int lane) {
+  const int pg = tile * 4 + lane;
+  int id = -1;
+  if (lane < 4 && pg < npages && ind_lo >= 0 && ind_lo + pg < p.num_indices)
+    id = p.kv_indices[ind_lo + pg];
+  return id;
+}
+
+// Pages of one K/V tile, resolved from the page ids in lanes 0-3 of `pid`
+// (absent or invalid pages: zero valid tokens).
+struct TilePages {
   int page[4], ntok[4];
+};
+
+__device__ __forceinline__ TilePages tile_pages(const PrefillParams& p, int pid,
+                                                int npages, int last, int tile) {
+  TilePages tp;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int pg = tile * 4 + j;
-    int id = -1;
-    if (pg < npages && ind_lo >= 0 && ind_lo + pg < p.num_indices) {
-      id = uniform(load_invariant(p.kv_indices + ind_lo + pg));
-      if (id >= p.num_pages) id = -1;
-    }
-    page[j] = id < 0 ? 0 : id;
-    ntok[j] = id < 0 ? 0 : (pg == npages - 1 ? last : kPage);
+    int id = __builtin_amdgcn_readlane(pid, j);
+    if (id >= p.num_pages) id = -1;
+    tp.page[j] = id < 0 ? 0 : id;
+    tp.ntok[j] = id < 0 ? 0 : (pg == npages - 1 ? last : kPage);
   }
+  return tp;
+}
+
+// Issue the global loads of one half of a K/V tile (V = false: K rows,
+// true: V rows) -- always the same number of loads: missing pages are
+// zero-sized buffers.  The e4m3 page scales travel with the K half.
+template <int D, bool BF16, bool FP8, int RB, bool V>
+__device__ __forceinline__ void load_half(TileRegs<D, BF16, FP8, RB>& tr,
+                                          const PrefillParams& p, int h,
+                                          const TilePages& tp, int wave,
+                                          int lane) {
+  using C = PrefillCfg<D, BF16, FP8, RB>;
 #pragma unroll
   for (int k = 0; k < C::CPT; ++k) {
     const int c = lane + 64 * wave + 256 * k;
     const int tok = c / (D / 8);
     const int d0 = (c % (D / 8)) * 8;
-    // the 64 chunks of a wave lie in one page: j is wave-uniform
-    const int j = uniform((64 * wave + 256 * k) / (D / 8) / kPage);
-    const int pj = j == 0 ? page[0] : j == 1 ? page[1] : j == 2 ? page[2] : page[3];
-    const int nj = j == 0 ? ntok[0] : j == 1 ? ntok[1] : j == 2 ? ntok[2] : ntok[3];
-    const uint8_t* kb =
-        p.cache + ((int64_t)pj * 2 * p.hkv + h) * (int64_t)C::PAGE_BYTES;
-    const uint8_t* vb = kb + (int64_t)p.hkv * C::PAGE_BYTES;
-    const uint32_t bytes = (uint32_t)(nj * D * C::ESZ);
+    // the 64 chunks of a wave lie in one page of the tile: page j is k for
+    // D = 128 and 2 k + wave / 2 for D = 64 (wave < 4)
+    constexpr int KPT = 256 / (D / 8) / kPage;  // pages per chunk step
+    const int j = k * KPT + (int)((64u * (unsigned)(wave & 3)) / (D / 8) / kPage);
+    int pj = tp.page[k * KPT], nj = tp.ntok[k * KPT];
+    if constexpr (KPT > 1) {
+      pj = uniform(j == k * KPT ? pj : tp.page[k * KPT + 1]);
+      nj = uniform(j == k * KPT ? nj : tp.ntok[k * KPT + 1]);
+    }
+    const uint8_t* base = p.cache + (((int64_t)pj * 2 + (V ? 1 : 0)) * p.hkv + h) *
+                                        (int64_t)C::PAGE_BYTES;
+    const __amdgpu_buffer_rsrc_t r = make_rsrc(base, (uint32_t)(nj * D * C::ESZ));
     const uint32_t off = (uint32_t)(((tok % kPage) * D + d0) * C::ESZ);
+    typename C::Raw x;
     if constexpr (FP8) {
-      tr.k[k] = buf_load8(make_rsrc(kb, bytes), off);
-      tr.v[k] = buf_load8(make_rsrc(vb, bytes), off);
+      x = buf_load8(r, off);
     } else {
-      tr.k[k] = buf_load16(make_rsrc(kb, bytes), off);
-      tr.v[k] = buf_load16(make_rsrc(vb, bytes), off);
+      x = buf_load16(r, off);
+    }
+    if constexpr (V) {
+      tr.v[k] = x;
+    } else {
+      tr.k[k] = x;
     }
   }
-  if constexpr (FP8) {
+  if constexpr (FP8 && !V) {
     tr.sc = 0.f;
     if (lane < 8) {
       const int j = lane & 3;
-      const int pj = j == 0 ? page[0] : j == 1 ? page[1] : j == 2 ? page[2] : page[3];
-      const int nj = j == 0 ? ntok[0] : j == 1 ? ntok[1] : j == 2 ? ntok[2] : ntok[3];
+      const int pj = j == 0 ? tp.page[0] : j == 1 ? tp.page[1] : j == 2 ? tp.page[2] : tp.page[3];
+      const int nj = j == 0 ? tp.ntok[0] : j == 1 ? tp.ntok[1] : j == 2 ? tp.ntok[2] : tp.ntok[3];
       if (nj > 0) tr.sc = p.kv_scales[((int64_t)pj * 2 + (lane >> 2)) * p.hkv + h];
     }
   }
@@ -208,12 +240,17 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
   const int wave = uniform(threadIdx.x >> 6);
   const int col = lane & 31;   // row of the 32-row block this lane owns
   const int half = lane >> 5;  // k-half of the MFMA operands
-  const int h = blockIdx.y;
+  // Workgroup w runs KV head w % Hkv of item w / Hkv.  Workgroups are dealt
+  // to the 8 XCDs round-robin by id, so one KV head's work stays on one XCD
+  // (Hkv = 8) or a fixed pair of them, and the q-tiles that re-read the same
+  // K/V pages (and prefix pages shared between sequences) hit that XCD's L2.
+  const int h = (int)(blockIdx.x % (unsigned)p.hkv);
+  const int item = (int)(blockIdx.x / (unsigned)p.hkv);
   const int g = p.g;
   // a work list that does not match this launch is skipped, never followed
   // (every condition is uniform over the workgroup)
-  if ((int)blockIdx.x >= p.n_items || h >= p.hkv) return;
-  const int32_t* itp = reinterpret_cast<const int32_t*>(p.items + blockIdx.x);
+  if (item >= p.n_items) return;
+  const int32_t* itp = reinterpret_cast<const int32_t*>(p.items + item);
   const int b = uniform(load_invariant(itp + 0));
   if (b < 0 || b >= p.batch_size) return;
   const int qo_start = uniform(load_invariant(p.qo_indptr + b));
@@ -263,20 +300,32 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
     l[rb] = 0.f;
   }
 
+  // K/V tiles: tile t is staged into LDS buffer t & 1 at the top of
+  // iteration t, and tile t + 1's global loads are issued between iteration
+  // t's MFMAs (K rows during QK, V rows during PV), so they spread over the
+  // compute phase and have all of it to arrive.  Page ids run one tile ahead
+  // of the loads.
   TileRegs<D, BF16, FP8, RB> tr;
   float sc_cur = 0.f;  // e4m3 scales of the tile being computed (lanes 0-7)
+  int pid = fetch_page_ids(p, ind_lo, npages, 0, lane);
   if (n_tiles > 0) {
-    load_tile(tr, p, h, ind_lo, npages, last, 0, wave, lane);
-    store_tile(tr, ks[0], vs[0], wave, lane);
-    if constexpr (FP8) sc_cur = tr.sc;
+    const TilePages tp = tile_pages(p, pid, npages, last, 0);
+    load_half<D, BF16, FP8, RB, false>(tr, p, h, tp, wave, lane);
+    load_half<D, BF16, FP8, RB, true>(tr, p, h, tp, wave, lane);
   }
-  __syncthreads();
-  if (n_tiles > 1) load_tile(tr, p, h, ind_lo, npages, last, 1, wave, lane);
+  int pid_next = fetch_page_ids(p, ind_lo, npages, 1, lane);
 
   for (int t = 0; t < n_tiles; ++t) {
     const int cur = t & 1;
     const uint16_t* kt = ks[cur];
     const uint16_t* vt = vs[cur];
+    store_tile(tr, ks[cur], vs[cur], wave, lane);
+    if constexpr (FP8) sc_cur = tr.sc;
+    __syncthreads();
+    const bool more = t + 1 < n_tiles;
+    pid = pid_next;
+    pid_next = fetch_page_ids(p, ind_lo, npages, t + 2, lane);
+    const TilePages tp = tile_pages(p, pid, npages, last, t + 1);
 
     // ---- S^T = K . Q^T
     f32x16 s[RB][2];
@@ -291,6 +340,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) s[rb][mt] = mfma32<BF16>(a, qf[rb][ks_], s[rb][mt]);
       }
+      if (mt == 0 && more) load_half<D, BF16, FP8, RB, false>(tr, p, h, tp, wave, lane);
     }
 
     // ---- online softmax in log2 units; lane holds 32 of the tile's 64
@@ -354,6 +404,7 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
     // ---- O^T += V^T . P^T over 4 steps of 16 tokens
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
+      if (st == 1 && more) load_half<D, BF16, FP8, RB, true>(tr, p, h, tp, wave, lane);
       u32x4 pb[RB];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
@@ -384,13 +435,6 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
       }
     }
 
-    // ---- stage tile t + 1 into the other buffer, then fetch tile t + 2
-    if (t + 1 < n_tiles) {
-      store_tile(tr, ks[cur ^ 1], vs[cur ^ 1], wave, lane);
-      if constexpr (FP8) sc_cur = tr.sc;
-    }
-    __syncthreads();
-    if (t + 2 < n_tiles) load_tile(tr, p, h, ind_lo, npages, last, t + 2, wave, lane);
   }
 
   // ---- epilogue: O^T / l, lane's row, 4 consecutive d per register quad
@@ -548,6 +592,8 @@ int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
     return set_error(PAGEDATTN_ERR_UNSUPPORTED,
                      "%s: sm_scale must be a positive finite number", who);
   if (plan->n_items == 0) return PAGEDATTN_OK;
+  if ((int64_t)plan->n_items * plan->hkv > INT32_MAX)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: too many work items", who);
   if (!q || !qo_indptr || !paged_kv_cache || !kv_indices || !kv_indptr ||
       !kv_last_page_len || !out)
     return set_error(PAGEDATTN_ERR_INVALID, "%s: null pointer", who);
@@ -582,7 +628,7 @@ int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
   p.causal = causal ? 1 : 0;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   PrefillFn fn = pick_prefill(plan->d, q_dtype == PAGEDATTN_BF16, fp8);
-  hipLaunchKernelGGL(fn, dim3(plan->n_items, plan->hkv), dim3(256), 0,
+  hipLaunchKernelGGL(fn, dim3(plan->n_items * plan->hkv), dim3(256), 0,
                      (hipStream_t)stream, p);
   return check_launch(who);
 }
