@@ -78,35 +78,61 @@ __device__ __forceinline__ uint32_t e4m3x2_to16(uint32_t w) {
   }
 }
 
+// Waves per workgroup: 8 (two per SIMD) share every K/V tile loaded into
+// LDS, which halves the global-to-LDS traffic per MFMA against 4 waves.
+constexpr int kPrefillWaves = 8;
+
 template <int D, bool BF16, bool FP8, int RB>
 struct PrefillCfg {
   static constexpr int ESZ = FP8 ? 1 : 2;
   static constexpr int BN = 64;             // kv tokens per tile
-  static constexpr int ROWS = 4 * 32 * RB;  // rows per workgroup
+  static constexpr int WAVES = kPrefillWaves;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int ROWS = WAVES * 32 * RB;  // rows per workgroup
   static constexpr int KS = D / 16;         // QK k-steps
   static constexpr int DT = D / 32;         // PV d tiles
-  // LDS row strides (elements): K rows read 16 B per lane at one column
-  // (conflict-free for 16 consecutive rows when the stride is 4 mod 64
-  // dwords); V rows are read 4 at a time by the transpose read (disjoint
-  // 8-dword bank ranges when the stride is 8 mod 64 dwords).
-  static constexpr int KSTR = D + 8;
-  static constexpr int VSTR = D + 16;
+  // LDS tiles are unpadded rows of ROWB bytes (16-bit elements) whose
+  // 16-byte chunks are XOR-swizzled per row (see swz), so whole 1 KiB runs
+  // can be written by direct-to-LDS loads and both read patterns below are
+  // free of bank conflicts.
+  static constexpr int ROWB = D * 2;
+  static constexpr int TILEB = BN * ROWB;  // bytes of one K or V tile
   static constexpr int CHUNKS = BN * D / 8;   // 16-byte (bf16) chunks per tile
-  static constexpr int CPT = CHUNKS / 256;    // chunks per thread
+  static constexpr int CPT = CHUNKS / THREADS;  // chunks per thread
   static constexpr int PAGE_BYTES = kPage * D * ESZ;
   using Raw = typename std::conditional<FP8, u32x2, u32x4>::type;
 };
 
+// Chunk swizzle of LDS row r: chunk c of the row is stored at position
+// c ^ swz(r).  D = 128 (16 chunks of 16 B per row): 16 consecutive rows get
+// 16 distinct positions for one chunk (K operand reads, one chunk per lane
+// and row), and 4 consecutive rows never collide for a chunk pair {2i,
+// 2i + 1} (V transpose reads).  D = 64 (8 chunks): the same with 8 rows.
+template <int D>
+__device__ __forceinline__ int swz(int r) {
+  if constexpr (D == 128) {
+    return ((r & 7) << 1) | ((r >> 3) & 1);
+  } else {
+    return ((r & 3) << 1) | ((r >> 2) & 1);
+  }
+}
+
+template <int D>
+__device__ __forceinline__ int lds_off(int r, int c) {
+  return r * (D * 2) + ((c ^ swz<D>(r)) << 4);
+}
+
+// Registers staging one half (K rows or V rows) of an e4m3 K/V tile between
+// its global loads and its converting LDS store.
 template <int D, bool BF16, bool FP8, int RB>
-struct TileRegs {
+struct HalfRegs {
   using C = PrefillCfg<D, BF16, FP8, RB>;
-  typename C::Raw k[C::CPT];
-  typename C::Raw v[C::CPT];
-  float sc;  // e4m3 pools: lanes 0-3 the K scales, 4-7 the V scales of the tile's pages
+  u32x2 x[C::CPT];
+  float sc;  // lane j < 4 holds the scale of the tile's page j
 };
 
 // Page ids of tile `tile` as a vector load: lane j < 4 gets the id of the
-// tile's page j (-1 past the sequence).  Issued one tile ahead of the K/V
+// tile's page j (-1 past the sequence).  Issued a tile ahead of the K/V
 // loads that use it, it is waited on with the in-order vector counter, so
 // no K/V load ever waits for a page-id fetch.
 __device__ __forceinline__ int fetch_page_ids(const PrefillParams& p,
@@ -119,102 +145,92 @@ __device__ __forceinline__ int fetch_page_ids(const PrefillParams& p,
   return id;
 }
 
-// Pages of one K/V tile, resolved from the page ids in lanes 0-3 of `pid`
-// (absent or invalid pages: zero valid tokens).
-struct TilePages {
-  int page[4], ntok[4];
-};
-
-__device__ __forceinline__ TilePages tile_pages(const PrefillParams& p, int pid,
-                                                int npages, int last, int tile) {
-  TilePages tp;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int pg = tile * 4 + j;
-    int id = __builtin_amdgcn_readlane(pid, j);
-    if (id >= p.num_pages) id = -1;
-    tp.page[j] = id < 0 ? 0 : id;
-    tp.ntok[j] = id < 0 ? 0 : (pg == npages - 1 ? last : kPage);
-  }
-  return tp;
-}
-
-// Issue the global loads of one half of a K/V tile (V = false: K rows,
-// true: V rows) -- always the same number of loads: missing pages are
-// zero-sized buffers.  The e4m3 page scales travel with the K half.
+// Buffer resource of the K (V = false) or V block of tile page j, sized to
+// its valid tokens: absent pages and slots past last_page_len read as zero.
 template <int D, bool BF16, bool FP8, int RB, bool V>
-__device__ __forceinline__ void load_half(TileRegs<D, BF16, FP8, RB>& tr,
-                                          const PrefillParams& p, int h,
-                                          const TilePages& tp, int wave,
-                                          int lane) {
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(
+    const PrefillParams& p, int h, int pid, int npages, int last, int tile,
+    int j) {
   using C = PrefillCfg<D, BF16, FP8, RB>;
+  int id = __builtin_amdgcn_readlane(pid, j);
+  if (id >= p.num_pages) id = -1;
+  const int pg = tile * 4 + j;
+  const int ntok = id < 0 ? 0 : (pg == npages - 1 ? last : kPage);
+  const uint8_t* base =
+      p.cache + (((int64_t)(id < 0 ? 0 : id) * 2 + (V ? 1 : 0)) * p.hkv + h) *
+                    (int64_t)C::PAGE_BYTES;
+  return make_rsrc(base, (uint32_t)(ntok * D * C::ESZ));
+}
+
+// bf16/fp16 pools: direct-to-LDS loads of one half of a K/V tile.  Wave w's
+// k-th load fills the 1 KiB block 8 k + w of the tile (lane i -> bytes
+// [16 i, 16 i + 16) of the block), so each lane fetches the global chunk
+// that the swizzle puts at its position.
+template <int D, bool BF16, bool FP8, int RB, bool V>
+__device__ __forceinline__ void dma_half(const PrefillParams& p, int h,
+                                         int pid, int npages, int last,
+                                         int tile, uint8_t* lds, int wave,
+                                         int lane) {
+  using C = PrefillCfg<D, BF16, FP8, RB>;
+  constexpr int RPB = 1024 / C::ROWB;   // rows per 1 KiB block
+  constexpr int CPR = C::ROWB / 16;     // chunks per row
+  constexpr int NK = C::TILEB / 1024 / C::WAVES;
 #pragma unroll
-  for (int k = 0; k < C::CPT; ++k) {
-    const int c = lane + 64 * wave + 256 * k;
-    const int tok = c / (D / 8);
-    const int d0 = (c % (D / 8)) * 8;
-    // the 64 chunks of a wave lie in one page of the tile: page j is k for
-    // D = 128 and 2 k + wave / 2 for D = 64 (wave < 4)
-    constexpr int KPT = 256 / (D / 8) / kPage;  // pages per chunk step
-    const int j = k * KPT + (int)((64u * (unsigned)(wave & 3)) / (D / 8) / kPage);
-    int pj = tp.page[k * KPT], nj = tp.ntok[k * KPT];
-    if constexpr (KPT > 1) {
-      pj = uniform(j == k * KPT ? pj : tp.page[k * KPT + 1]);
-      nj = uniform(j == k * KPT ? nj : tp.ntok[k * KPT + 1]);
-    }
-    const uint8_t* base = p.cache + (((int64_t)pj * 2 + (V ? 1 : 0)) * p.hkv + h) *
-                                        (int64_t)C::PAGE_BYTES;
-    const __amdgpu_buffer_rsrc_t r = make_rsrc(base, (uint32_t)(nj * D * C::ESZ));
-    const uint32_t off = (uint32_t)(((tok % kPage) * D + d0) * C::ESZ);
-    typename C::Raw x;
-    if constexpr (FP8) {
-      x = buf_load8(r, off);
-    } else {
-      x = buf_load16(r, off);
-    }
-    if constexpr (V) {
-      tr.v[k] = x;
-    } else {
-      tr.k[k] = x;
-    }
-  }
-  if constexpr (FP8 && !V) {
-    tr.sc = 0.f;
-    if (lane < 8) {
-      const int j = lane & 3;
-      const int pj = j == 0 ? tp.page[0] : j == 1 ? tp.page[1] : j == 2 ? tp.page[2] : tp.page[3];
-      const int nj = j == 0 ? tp.ntok[0] : j == 1 ? tp.ntok[1] : j == 2 ? tp.ntok[2] : tp.ntok[3];
-      if (nj > 0) tr.sc = p.kv_scales[((int64_t)pj * 2 + (lane >> 2)) * p.hkv + h];
-    }
+  for (int k = 0; k < NK; ++k) {
+    const int blk = C::WAVES * k + wave;
+    const int row0 = blk * RPB;
+    const int j = uniform(row0 / kPage);  // page of the block within the tile
+    const __amdgpu_buffer_rsrc_t r =
+        page_rsrc<D, BF16, FP8, RB, V>(p, h, pid, npages, last, tile, j);
+    const int row = row0 + lane / CPR;
+    const int c = (lane % CPR) ^ swz<D>(row);
+    const uint32_t off = (uint32_t)((row % kPage) * C::ROWB + c * 16);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)(lds + blk * 1024), 16, off,
+        0, 0, 0);
   }
 }
 
-template <int D, bool BF16, bool FP8, int RB>
-__device__ __forceinline__ void store_tile(const TileRegs<D, BF16, FP8, RB>& tr,
-                                           uint16_t* ks, uint16_t* vs,
-                                           int wave, int lane) {
+// e4m3 pools: register loads of one half of a K/V tile (8 elements per
+// lane and load) plus the four page scales.
+template <int D, bool BF16, bool FP8, int RB, bool V>
+__device__ __forceinline__ void load_half(HalfRegs<D, BF16, FP8, RB>& hr,
+                                          const PrefillParams& p, int h,
+                                          int pid, int npages, int last,
+                                          int tile, int wave, int lane) {
   using C = PrefillCfg<D, BF16, FP8, RB>;
 #pragma unroll
   for (int k = 0; k < C::CPT; ++k) {
-    const int c = lane + 64 * wave + 256 * k;
+    const int c = lane + 64 * wave + C::THREADS * k;
     const int tok = c / (D / 8);
     const int d0 = (c % (D / 8)) * 8;
-    u32x4 kx, vx;
-    if constexpr (FP8) {
-      kx[0] = e4m3x2_to16<BF16, false>(tr.k[k][0]);
-      kx[1] = e4m3x2_to16<BF16, true>(tr.k[k][0]);
-      kx[2] = e4m3x2_to16<BF16, false>(tr.k[k][1]);
-      kx[3] = e4m3x2_to16<BF16, true>(tr.k[k][1]);
-      vx[0] = e4m3x2_to16<BF16, false>(tr.v[k][0]);
-      vx[1] = e4m3x2_to16<BF16, true>(tr.v[k][0]);
-      vx[2] = e4m3x2_to16<BF16, false>(tr.v[k][1]);
-      vx[3] = e4m3x2_to16<BF16, true>(tr.v[k][1]);
-    } else {
-      kx = tr.k[k];
-      vx = tr.v[k];
-    }
-    *reinterpret_cast<u32x4*>(ks + tok * C::KSTR + d0) = kx;
-    *reinterpret_cast<u32x4*>(vs + tok * C::VSTR + d0) = vx;
+    // the 64 chunks of a wave lie in one page of the tile
+    const int j = uniform((64 * wave + C::THREADS * k) / (D / 8) / kPage);
+    const __amdgpu_buffer_rsrc_t r =
+        page_rsrc<D, BF16, FP8, RB, V>(p, h, pid, npages, last, tile, j);
+    hr.x[k] = buf_load8(r, (uint32_t)((tok % kPage) * D + d0));
+  }
+  hr.sc = 0.f;
+  if (lane < 4 && pid >= 0 && pid < p.num_pages)
+    hr.sc = p.kv_scales[((int64_t)pid * 2 + (V ? 1 : 0)) * p.hkv + h];
+}
+
+// e4m3 -> 16-bit conversion and store of a staged half tile, swizzled.
+template <int D, bool BF16, bool FP8, int RB>
+__device__ __forceinline__ void store_half(const HalfRegs<D, BF16, FP8, RB>& hr,
+                                           uint8_t* lds, int wave, int lane) {
+  using C = PrefillCfg<D, BF16, FP8, RB>;
+#pragma unroll
+  for (int k = 0; k < C::CPT; ++k) {
+    const int c = lane + 64 * wave + C::THREADS * k;
+    const int tok = c / (D / 8);
+    const int chunk = c % (D / 8);
+    u32x4 x;
+    x[0] = e4m3x2_to16<BF16, false>(hr.x[k][0]);
+    x[1] = e4m3x2_to16<BF16, true>(hr.x[k][0]);
+    x[2] = e4m3x2_to16<BF16, false>(hr.x[k][1]);
+    x[3] = e4m3x2_to16<BF16, true>(hr.x[k][1]);
+    *reinterpret_cast<u32x4*>(lds + lds_off<D>(tok, chunk)) = x;
   }
 }
 
@@ -229,12 +245,16 @@ __device__ __forceinline__ float lane_value(float v, int i) {
 constexpr float kRescaleSlack = 8.f;
 
 template <int D, bool BF16, bool FP8, int RB>
-__global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
+__global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillParams p) {
   using C = PrefillCfg<D, BF16, FP8, RB>;
   constexpr int BN = C::BN;
-  // two K/V tile buffers: tile t + 1 is written while tile t is read
-  __shared__ __attribute__((aligned(16))) uint16_t ks[2][BN * C::KSTR];
-  __shared__ __attribute__((aligned(16))) uint16_t vs[2][BN * C::VSTR];
+  // Two stages, each a K tile then a V tile.  Tile t lives in stage t & 1;
+  // tile t + 1 is loaded into the other stage while tile t is computed.
+  // Separate arrays (not one indexed array) let the compiler see that the
+  // direct-to-LDS loads into one stage never alias reads of the other, so it
+  // does not wait for them before those reads.
+  __shared__ __attribute__((aligned(1024))) uint8_t stage0[2 * C::TILEB];
+  __shared__ __attribute__((aligned(1024))) uint8_t stage1[2 * C::TILEB];
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -300,32 +320,53 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
     l[rb] = 0.f;
   }
 
-  // K/V tiles: tile t is staged into LDS buffer t & 1 at the top of
-  // iteration t, and tile t + 1's global loads are issued between iteration
-  // t's MFMAs (K rows during QK, V rows during PV), so they spread over the
-  // compute phase and have all of it to arrive.  Page ids run one tile ahead
-  // of the loads.
-  TileRegs<D, BF16, FP8, RB> tr;
-  float sc_cur = 0.f;  // e4m3 scales of the tile being computed (lanes 0-7)
+  // Per-lane LDS byte offsets (swizzled) of the MFMA operand reads, fixed
+  // for the whole loop: K rows 32 mt + col, chunk 2 ks + half (mt adds
+  // 32 rows, which keeps the swizzle); V transpose reads at rows
+  // 16 st + 4 half + L/4 (+8), chunk 4 dt + 2 (qg & 1) + (L & 3) / 2.
+  int koff[C::KS];
+#pragma unroll
+  for (int ks_ = 0; ks_ < C::KS; ++ks_) koff[ks_] = lds_off<D>(col, 2 * ks_ + half);
+  const int L = lane & 15;
+  const int qg = lane >> 4;
+  int voff[C::DT][2];
+#pragma unroll
+  for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+    for (int hi = 0; hi < 2; ++hi)
+      voff[dt][hi] = C::TILEB +
+                     lds_off<D>(4 * half + (L >> 2) + 8 * hi,
+                                4 * dt + 2 * (qg & 1) + ((L & 3) >> 1)) +
+                     8 * (L & 1);
+
+  HalfRegs<D, BF16, FP8, RB> kr, vr;  // e4m3 staging only
+  float ksc_l = 0.f, vsc_l = 0.f;     // e4m3 scales of the computed tile
   int pid = fetch_page_ids(p, ind_lo, npages, 0, lane);
   if (n_tiles > 0) {
-    const TilePages tp = tile_pages(p, pid, npages, last, 0);
-    load_half<D, BF16, FP8, RB, false>(tr, p, h, tp, wave, lane);
-    load_half<D, BF16, FP8, RB, true>(tr, p, h, tp, wave, lane);
+    if constexpr (FP8) {
+      load_half<D, BF16, FP8, RB, false>(kr, p, h, pid, npages, last, 0, wave, lane);
+      load_half<D, BF16, FP8, RB, true>(vr, p, h, pid, npages, last, 0, wave, lane);
+    } else {
+      dma_half<D, BF16, FP8, RB, false>(p, h, pid, npages, last, 0, stage0, wave, lane);
+      dma_half<D, BF16, FP8, RB, true>(p, h, pid, npages, last, 0, stage0 + C::TILEB,
+                                       wave, lane);
+    }
   }
   int pid_next = fetch_page_ids(p, ind_lo, npages, 1, lane);
 
-  for (int t = 0; t < n_tiles; ++t) {
-    const int cur = t & 1;
-    const uint16_t* kt = ks[cur];
-    const uint16_t* vt = vs[cur];
-    store_tile(tr, ks[cur], vs[cur], wave, lane);
-    if constexpr (FP8) sc_cur = tr.sc;
+  // Iteration t: (e4m3: convert and store tile t) -- barrier -- issue tile
+  // t + 1's loads into the other stage, interleaved with tile t's MFMAs.
+  auto step = [&](int t, uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+    if constexpr (FP8) {
+      store_half<D, BF16, FP8, RB>(kr, cur, wave, lane);
+      store_half<D, BF16, FP8, RB>(vr, cur + C::TILEB, wave, lane);
+      ksc_l = kr.sc;
+      vsc_l = vr.sc;
+    }
     __syncthreads();
     const bool more = t + 1 < n_tiles;
     pid = pid_next;
     pid_next = fetch_page_ids(p, ind_lo, npages, t + 2, lane);
-    const TilePages tp = tile_pages(p, pid, npages, last, t + 1);
 
     // ---- S^T = K . Q^T
     f32x16 s[RB][2];
@@ -335,12 +376,18 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
       for (int ks_ = 0; ks_ < C::KS; ++ks_) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(
-            kt + (32 * mt + col) * C::KSTR + 16 * ks_ + 8 * half);
+        const u32x4 a =
+            *reinterpret_cast<const u32x4*>(cur + 32 * mt * C::ROWB + koff[ks_]);
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) s[rb][mt] = mfma32<BF16>(a, qf[rb][ks_], s[rb][mt]);
       }
-      if (mt == 0 && more) load_half<D, BF16, FP8, RB, false>(tr, p, h, tp, wave, lane);
+      if (mt == 0 && more) {
+        if constexpr (FP8) {
+          load_half<D, BF16, FP8, RB, false>(kr, p, h, pid, npages, last, t + 1, wave, lane);
+        } else {
+          dma_half<D, BF16, FP8, RB, false>(p, h, pid, npages, last, t + 1, nxt, wave, lane);
+        }
+      }
     }
 
     // ---- online softmax in log2 units; lane holds 32 of the tile's 64
@@ -350,8 +397,8 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
     float ksc[4], vsc[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      ksc[i] = FP8 ? lane_value(sc_cur, i) * p.scale_log2 : p.scale_log2;
-      vsc[i] = FP8 ? lane_value(sc_cur, 4 + i) : 1.f;
+      ksc[i] = FP8 ? lane_value(ksc_l, i) * p.scale_log2 : p.scale_log2;
+      vsc[i] = FP8 ? lane_value(vsc_l, i) : 1.f;
     }
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
@@ -404,7 +451,14 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
     // ---- O^T += V^T . P^T over 4 steps of 16 tokens
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      if (st == 1 && more) load_half<D, BF16, FP8, RB, true>(tr, p, h, tp, wave, lane);
+      if (st == 1 && more) {
+        if constexpr (FP8) {
+          load_half<D, BF16, FP8, RB, true>(vr, p, h, pid, npages, last, t + 1, wave, lane);
+        } else {
+          dma_half<D, BF16, FP8, RB, true>(p, h, pid, npages, last, t + 1, nxt + C::TILEB,
+                                           wave, lane);
+        }
+      }
       u32x4 pb[RB];
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
@@ -415,18 +469,12 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
                                      s[rb][st >> 1][r0 + 1] * vsc[st]);
         }
       }
-      // transpose reads: lane (group qg, index L) points at
-      // V[16 st + 4 half + L/4 (+8)][32 dt + 16 (qg & 1) + 4 (L & 3)]
-      const int L = lane & 15;
-      const int qg = lane >> 4;
-      const int vrow = 16 * st + 4 * half + (L >> 2);
-      const int vcol = 16 * (qg & 1) + 4 * (L & 3);
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) {
         const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(vt + vrow * C::VSTR + 32 * dt + vcol));
+            (lds_i16x4*)(cur + 16 * st * C::ROWB + voff[dt][0]));
         const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(vt + (vrow + 8) * C::VSTR + 32 * dt + vcol));
+            (lds_i16x4*)(cur + 16 * st * C::ROWB + voff[dt][1]));
         const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
         const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
         const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
@@ -434,7 +482,11 @@ __global__ void __launch_bounds__(256, 2) prefill_kernel(PrefillParams p) {
         for (int rb = 0; rb < RB; ++rb) o[rb][dt] = mfma32<BF16>(a, pb[rb], o[rb][dt]);
       }
     }
-
+  };
+  for (int t = 0; t < n_tiles; t += 2) {
+    step(t, stage0, stage1);
+    if (t + 1 >= n_tiles) break;
+    step(t + 1, stage1, stage0);
   }
 
   // ---- epilogue: O^T / l, lane's row, 4 consecutive d per register quad
@@ -481,7 +533,7 @@ static PrefillFn pick_prefill(int d, bool bf16, bool fp8) {
   return fp8 ? prefill_fn<128, false, true>() : prefill_fn<128, false, false>();
 }
 
-constexpr int kPrefillRows = 4 * 32 * kPrefillRB;
+constexpr int kPrefillRows = kPrefillWaves * 32 * kPrefillRB;
 
 }  // namespace pa
 
@@ -628,7 +680,7 @@ int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
   p.causal = causal ? 1 : 0;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   PrefillFn fn = pick_prefill(plan->d, q_dtype == PAGEDATTN_BF16, fp8);
-  hipLaunchKernelGGL(fn, dim3(plan->n_items * plan->hkv), dim3(256), 0,
+  hipLaunchKernelGGL(fn, dim3(plan->n_items * plan->hkv), dim3(64 * kPrefillWaves), 0,
                      (hipStream_t)stream, p);
   return check_launch(who);
 }
