@@ -19,6 +19,7 @@ Prints ONE JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import os
 import sys
@@ -77,47 +78,31 @@ def bench_decode(w, args, dev, dtype, label, cpu_sample: int = 0):
     outs = [torch.empty((w.meta.batch_size, w.hq, w.d), dtype=dtype, device=dev)
             for _ in range(reps)]
 
-    def step(i, ev=None):
+    def step(i):
         # the decode step: new token's K/V appended at kv_len - 1, then
-        # attention, in one launch (pagedattn_decode_run_append)
+        # attention, in one launch (pagedattn_decode_run_append) plus the
+        # split-KV merge launch when the plan cut sequences
         t = inst[i % reps]
-        if ev is not None:
-            ev[0].record()
         dw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps], append_key=t.k_new,
                append_value=t.v_new)
-        if ev is not None:
-            ev[1].record()
 
     for i in range(args.warmup):
         step(i)
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
     for i in range(args.steps):
-        step(args.warmup + i, evs[i])
+        step(args.warmup + i)
     end.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
-    attn_ms = [a.elapsed_time(b) for a, b in evs]
-    # attention launches back to back (replicas rotate, so no launch reuses
-    # cached KV): HIP events around the whole loop on the launch stream
-    start.record()
-    for i in range(args.steps):
-        t = inst[i % reps]
-        dw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps])
-    end.record()
-    torch.cuda.synchronize()
-    attn_avg = start.elapsed_time(end) / args.steps
+    attn_avg = total_ms / args.steps
     res = {
         "workload": label,
         "ms_per_step": total_ms / args.steps,
         "step_GBps": alg_step / (total_ms / args.steps * 1e-3) / 1e9,
         "attn_ms_avg": attn_avg,
-        "attn_ms_in_step_median": float(np.median(attn_ms)),
         "attn_GBps": alg_attn / (attn_avg * 1e-3) / 1e9,
         "alg_bytes_attn": alg_attn,
         "alg_bytes_step": alg_step,
@@ -152,30 +137,24 @@ def bench_prefill(w, args, dev, dtype, label):
             q_data_type=dtype, causal=True)
     out = torch.empty_like(t.q)
 
-    def step(ev=None):
+    def step():
         pagedattn.append_paged_kv_cache(t.k_new, t.v_new, t.batch_indices, t.positions, t.pool,
                                         t.kv_indices, t.kv_indptr, t.kv_last_page_len,
                                         kv_layout="HND", kv_scales=t.scales)
-        if ev is not None:
-            ev[0].record()
         pw.run(t.q, t.pool, kv_scales=t.scales, out=out)
-        if ev is not None:
-            ev[1].record()
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     start.record()
     for i in range(args.steps):
-        step(evs[i])
+        step()
     end.record()
     torch.cuda.synchronize()
     total_ms = start.elapsed_time(end)
-    attn = [a.elapsed_time(b) for a, b in evs]
+    # attention launches back to back: HIP events around the loop
     start.record()
     for _ in range(args.steps):
         pw.run(t.q, t.pool, kv_scales=t.scales, out=out)
@@ -186,7 +165,6 @@ def bench_prefill(w, args, dev, dtype, label):
         "workload": label,
         "ms_per_step": total_ms / args.steps,
         "attn_ms_avg": avg,
-        "attn_ms_in_step_median": float(np.median(attn)),
         "attn_TFLOPs": flops / (avg * 1e-3) / 1e12,
         "alg_flops_attn": flops,
         "rows": int(w.meta.nnz),
@@ -266,6 +244,20 @@ def copy_calibration(dev, nbytes: int = 1 << 30, reps: int = 3) -> dict:
             "GBps": 2 * nbytes / (ms * 1e-3) / 1e9}
 
 
+def load_traffic() -> dict | None:
+    """HBM bytes per decode step measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    runs of this bench (scaled by the plain-copy calibration), as committed in
+    profiles/; None when absent."""
+    path = os.path.join(ROOT, "profiles", "decode_tinyllama_b256_hbm_traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return None
+    d["source"] = os.path.relpath(path, ROOT)
+    return d
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,6 +299,14 @@ def main() -> int:
         extra["llama3_8b_long_decode"] = {k: lr[k] for k in (
             "ms_per_step", "attn_ms_avg", "attn_GBps", "attn_frac", "alg_bytes_attn",
             "split_pages", "batch", "kv_tokens")}
+        # the planner's own balanced partition of the same batch
+        lb = bench_decode(dataclasses.replace(lw, split_pages=0),
+                          argparse.Namespace(steps=max(5, args.steps // 3), warmup=2), dev,
+                          dtype, "llama3_8b_long_decode.balanced")
+        log(f"llama3_8b_long_decode (balanced split): {lb['attn_GBps']:.0f} GB/s "
+            f"({100 * lb['attn_frac']:.1f}%)")
+        extra["llama3_8b_long_decode.balanced"] = {k: lb[k] for k in (
+            "ms_per_step", "attn_GBps", "attn_frac", "split_pages")}
         pa_ = argparse.Namespace(steps=max(5, args.steps // 2), warmup=2)
         pr = bench_prefill(W.llama3_8b_prefill(seed=args.seed), pa_, dev, dtype,
                            "llama3_8b_prefill")
@@ -325,6 +325,7 @@ def main() -> int:
             "prefill": p5,
         }
     cal = copy_calibration(dev)
+    traffic = load_traffic()
     log(f"copy calibration: {cal['GBps']:.0f} GB/s (read+write)")
 
     line = {
@@ -351,14 +352,16 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode attention launch (pagedattn decode_kernel<64,bf16>)",
-            "achieved": round(r["attn_GBps"], 2),
+            "kernel": "decode step launch: decode_kernel<64, bf16, append> (new token's K/V "
+                      "written, then attention) plus its split-KV merge launch",
+            "achieved": round(r["step_GBps"], 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(r["attn_frac"], 4),
-            "traffic": None,
-            "alg_bytes_per_launch": r["alg_bytes_attn"],
-            "avg_launch_ms": round(r["attn_ms_avg"], 5),
+            "frac": round(r["step_GBps"] / HBM_PEAK_GBS, 4),
+            "traffic": traffic.get("traffic_bytes_per_step") if traffic else None,
+            "traffic_source": traffic.get("source") if traffic else None,
+            "alg_bytes_per_launch": r["alg_bytes_step"],
+            "avg_launch_ms": round(r["ms_per_step"], 5),
         },
         "cpu_baseline": r.get("cpu"),
         "extra": extra,
