@@ -1,14 +1,17 @@
 // Paged decode attention for gfx950 (BatchDecodeWithPagedKVCacheWrapper,
 // src/models/llama.py:119-147 plan and :230-245 run).
 //
-// Work unit: one wave owns a list of items; an item is (page range of one
-// sequence, one KV head) for all g = Hq/Hkv query heads of that head, so
-// each K/V byte is read from HBM once.  Waves are independent: no barriers,
-// no cross-wave LDS merges, so one slow memory request stalls one wave only.
-// The host planner cuts the concatenated (sequence, head, page) stream into
-// equal shares per wave (or assigns whole sequences / fixed chunks to the
-// least-loaded wave); sequences cut in pieces write split partials that a
-// small merge launch combines.
+// Work unit: a head group of hg waves (hg KV heads, hg = 4, 2 or 1) owns a
+// list of items; an item is (page range of one sequence, KV heads h0 ..
+// h0 + hg - 1), wave i taking head h0 + i for all g = Hq/Hkv query heads of
+// that head, so each K/V byte is read from HBM once and a page's K (then V)
+// blocks of the group's heads are read as one contiguous run.  Waves are
+// independent: no barriers, no cross-wave LDS merges, so one slow memory
+// request stalls one wave only.  The host planner cuts the concatenated
+// (sequence, head group, page) stream into equal shares per group (or
+// assigns whole sequences / fixed chunks to the least-loaded group);
+// sequences cut in pieces write split partials that a small merge launch
+// combines.
 //
 // Per page pair (32 tokens) a wave does:
 //   S^T[32 tok x 16 heads] = K[tok x D] . Q^T      (v_mfma_f32_16x16x32, D/32 k-steps per page)

@@ -5,8 +5,9 @@
 // Work unit: a tile of ROWS query rows of one sequence and one KV head, where
 // a row is (query token, query head of the group): rows are token-major with
 // the g = Hq/Hkv heads of a token adjacent, so every K/V tile staged in LDS
-// serves all heads of the group.  A 256-thread workgroup runs 4 waves; wave w
-// owns RB blocks of 32 rows.  The KV loop walks 64-token tiles (4 pages):
+// serves all heads of the group.  A 512-thread workgroup runs 8 waves (two
+// per SIMD); wave w owns RB blocks of 32 rows.  The KV loop walks 64-token
+// tiles (4 pages):
 //
 //   S^T[64 tok x 32 rows] = K[tok x D] . Q^T          v_mfma_f32_32x32x16_bf16
 //   O^T[D x 32 rows]     += V^T[D x 64 tok] . P^T      (P stays in registers)
@@ -15,13 +16,14 @@
 // the B-operand layout that PV needs once the token order inside each
 // 16-token step is permuted the same way on both operands, so P never leaves
 // registers; a lane's row max / sum need one cross-half exchange.  K and V
-// tiles are staged row-major in LDS (coalesced 16-byte loads, 16-byte LDS
-// writes); the V^T operand is read with ds_read_b64_tr_b16, whose 16-lane
-// groups return the transposed 4x16 block, so no transposing writes exist.
-// Loads use buffer resources sized to each page's valid tokens: absent pages
-// and slots past last_page_len read as zero without touching memory.
-// Causal tiles entirely below the diagonal skip masking; tiles above the last
-// row's diagonal are never visited.
+// tiles are staged row-major in LDS by direct-to-LDS buffer loads (e4m3:
+// register loads converted to 16-bit on the way in) into unpadded rows whose
+// 16-byte chunks are XOR-swizzled per row; the V^T operand is read with
+// ds_read_b64_tr_b16, whose 16-lane groups return the transposed 4x16 block,
+// so no transposing writes exist.  Loads use buffer resources sized to each
+// page's valid tokens: absent pages and slots past last_page_len read as
+// zero without touching memory.  Causal tiles entirely below the diagonal
+// skip masking; tiles above the last row's diagonal are never visited.
 #include <algorithm>
 #include <climits>
 #include <cmath>
