@@ -126,6 +126,26 @@ int pagedattn_append_paged_kv_cache(
     const int32_t* kv_last_page_len, int32_t batch_size, int32_t num_kv_heads,
     int32_t head_dim, int32_t page_size, int32_t* error_flag, void* stream);
 
+/* flashinfer.apply_rope_pos_ids_inplace(q, k, positions, interleave=False,
+ * rope_scale, rope_theta) (src/models/llama.py:175-182) followed by
+ * flashinfer.append_paged_kv_cache (:188-210), in one launch: q
+ * [nnz, num_qo_heads, head_dim] and append_key are rotated in place over the
+ * full head (non-interleaved halves) exactly as
+ * pagedattn_apply_rope_pos_ids_inplace does, and the rotated K rows and the
+ * V rows are written to their page slots as pagedattn_append_paged_kv_cache
+ * does.  head_dim must be a multiple of 16.  Same metadata, error and e4m3
+ * contract as pagedattn_append_paged_kv_cache. */
+int pagedattn_rope_append_paged_kv_cache(
+    void* q, int64_t q_stride_n, int64_t q_stride_h, int32_t num_qo_heads,
+    void* append_key, const void* append_value, int64_t k_stride_n,
+    int64_t k_stride_h, int64_t v_stride_n, int64_t v_stride_h,
+    int32_t src_dtype, const int32_t* batch_indices, const int32_t* positions,
+    int32_t nnz, float rope_scale, float rope_theta, void* paged_kv_cache,
+    int32_t cache_dtype, const float* kv_scales, int32_t num_pages,
+    const int32_t* kv_indices, int32_t num_indices, const int32_t* kv_indptr,
+    int32_t batch_size, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+    int32_t* error_flag, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Plans.  pagedattn_plan_create/destroy manage the host object.
  * BatchDecodeWithPagedKVCacheWrapper.begin_forward(kv_indptr, kv_indices,
@@ -177,6 +197,28 @@ int pagedattn_decode_run_append(
     int64_t v_stride_n, int64_t v_stride_h, void* paged_kv_cache,
     int32_t kv_dtype, const float* kv_scales, int32_t num_pages,
     const int32_t* kv_indices, int32_t num_indices, const int32_t* kv_indptr,
+    const int32_t* kv_last_page_len, void* out, float* lse, float sm_scale,
+    void* stream);
+
+/* The whole attention of one decode step of the engine in one launch:
+ * flashinfer.apply_rope_pos_ids_inplace(q, k, positions, interleave=False,
+ * rope_scale, rope_theta) (src/models/llama.py:175-182), then
+ * pagedattn_decode_run_append's append + attention.  q and append_key are
+ * rotated in registers (they are read, not modified); the rotated new K row
+ * is what lands in the pool.  positions [B] int32 (device; NULL means
+ * kv_len_b - 1, the engine's decode positions) is each new token's position:
+ * RoPE angle, and page positions/16, slot positions%16 of the append (a
+ * position outside the sequence's pages is skipped).  Rotation math is the
+ * one of pagedattn_apply_rope_pos_ids_inplace, so the output and the pool
+ * equal (bit for bit) those of the three separate calls. */
+int pagedattn_decode_run_rope_append(
+    const pagedattn_plan* plan, const void* q, int64_t q_stride_n,
+    int64_t q_stride_h, int32_t q_dtype, const void* append_key,
+    const void* append_value, int64_t k_stride_n, int64_t k_stride_h,
+    int64_t v_stride_n, int64_t v_stride_h, const int32_t* positions,
+    float rope_scale, float rope_theta, void* paged_kv_cache, int32_t kv_dtype,
+    const float* kv_scales, int32_t num_pages, const int32_t* kv_indices,
+    int32_t num_indices, const int32_t* kv_indptr,
     const int32_t* kv_last_page_len, void* out, float* lse, float sm_scale,
     void* stream);
 

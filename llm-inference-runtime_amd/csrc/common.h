@@ -129,6 +129,48 @@ __device__ __forceinline__ uint32_t f32_to_e4m3x4(float a, float b, float c,
   return (uint32_t)w;
 }
 
+// RoPE (src/models/llama.py:175-182 via flashinfer.apply_rope_pos_ids_inplace):
+// angle of frequency i at position pos, inv_freq = theta^(-2i/rotary_dim),
+// pos / rope_scale, formed and reduced mod 2 pi in fp64 so that positions up
+// to 2^17 keep fp32 accuracy in the sin / cos.  Every kernel that rotates
+// uses these two functions, so fused and stand-alone rotations agree bit for
+// bit.
+__device__ __forceinline__ void rope_cos_sin(int pos, int i, int rotary_dim,
+                                             double inv_scale, double log2_theta,
+                                             float* c, float* s) {
+  const double inv_freq = exp2(-(double)(2 * i) / (double)rotary_dim * log2_theta);
+  double ang = (double)pos * inv_scale * inv_freq;
+  constexpr double kTwoPi = 6.283185307179586476925286766559;
+  ang -= kTwoPi * rint(ang * (1.0 / kTwoPi));
+  sincosf((float)ang, s, c);
+}
+
+// (x0, x1) rotated by the angle with cosine c and sine s, with one fixed
+// rounding order.
+__device__ __forceinline__ void rope_rotate(float x0, float x1, float c, float s,
+                                            float* y0, float* y1) {
+  *y0 = __builtin_fmaf(x0, c, -(x1 * s));
+  *y1 = __builtin_fmaf(x1, c, x0 * s);
+}
+
+// Eight consecutive 16-bit elements (u32x4) rotated against their partners
+// half a head away: lo holds elements i .. i+7, hi elements i+D/2 .. i+D/2+7.
+template <bool IS_BF16>
+__device__ __forceinline__ void rope8(u32x4& lo, u32x4& hi, const float (&c)[8],
+                                      const float (&s)[8]) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    float y[4];
+    rope_rotate(h2f<IS_BF16>((uint16_t)(lo[w] & 0xffffu)),
+                h2f<IS_BF16>((uint16_t)(hi[w] & 0xffffu)), c[2 * w], s[2 * w], &y[0],
+                &y[1]);
+    rope_rotate(h2f<IS_BF16>((uint16_t)(lo[w] >> 16)), h2f<IS_BF16>((uint16_t)(hi[w] >> 16)),
+                c[2 * w + 1], s[2 * w + 1], &y[2], &y[3]);
+    lo[w] = (uint32_t)f2h<IS_BF16>(y[0]) | ((uint32_t)f2h<IS_BF16>(y[2]) << 16);
+    hi[w] = (uint32_t)f2h<IS_BF16>(y[1]) | ((uint32_t)f2h<IS_BF16>(y[3]) << 16);
+  }
+}
+
 // wave-level reductions over lanes that differ in bits 4 and 5 (the four
 // 16-lane groups of a 16x16 MFMA tile).
 __device__ __forceinline__ float max_over_groups16(float v) {

@@ -69,6 +69,11 @@ struct DecodeParams {
   const uint16_t* k_new;
   const uint16_t* v_new;
   int64_t k_sn, k_sh, v_sn, v_sh;
+  // position of sequence b's new token: new_pos[b], or kv_len_b - 1 when
+  // new_pos is null; the fused append writes it to page new_pos / 16, slot
+  // new_pos % 16, and the fused RoPE rotates q and the new K row there
+  const int32_t* new_pos;
+  double rope_inv_scale, rope_log2_theta;
 };
 
 #ifndef DECODE_KV_POLICY
@@ -387,22 +392,17 @@ __device__ __forceinline__ u32x2 quant8(u32x4 x, float scale) {
 // append of flashinfer.append_paged_kv_cache at position kv_len - 1) and to
 // the wave's LDS slot `new_row`.  Lanes [0, D/8) move the K row, lanes
 // [32, 32 + D/8) the V row, 8 elements each.
+// With ROPE the K row is rotated first (position `pos`): lane c < D/16 takes
+// the chunk pair c, c + D/16 (elements i and i + D/2).
 template <int D, bool BF16, bool FP8>
-__device__ __forceinline__ void fused_append(const DecodeParams& p,
-                                             uint8_t* new_row, int b, int h,
-                                             int page, int slot, int lane) {
+__device__ __forceinline__ void put_chunk(const DecodeParams& p, uint8_t* new_row,
+                                          int h, int page, int slot, int is_v, int c,
+                                          u32x4 x) {
   using Tr = DecodeTraits<D, BF16, FP8>;
-  const int is_v = lane >> 5;
-  const int c = lane & 31;
-  if (c >= D / 8) return;
-  const uint16_t* src =
-      is_v ? p.v_new + (int64_t)b * p.v_sn + (int64_t)h * p.v_sh
-           : p.k_new + (int64_t)b * p.k_sn + (int64_t)h * p.k_sh;
   uint8_t* dst = const_cast<uint8_t*>(p.cache) +
                  (((int64_t)page * 2 + is_v) * p.hkv + h) * (int64_t)Tr::PAGE_BYTES +
                  ((int64_t)slot * D + 8 * c) * Tr::ESZ;
   uint8_t* lds = new_row + (is_v * D + 8 * c) * Tr::ESZ;
-  const u32x4 x = *reinterpret_cast<const u32x4*>(src + 8 * c);
   if constexpr (FP8) {
     const float scale =
         load_invariant(p.kv_scales + ((int64_t)page * 2 + is_v) * p.hkv + h);
@@ -415,7 +415,34 @@ __device__ __forceinline__ void fused_append(const DecodeParams& p,
   }
 }
 
-template <int D, bool BF16, bool FP8, bool APPEND>
+template <int D, bool BF16, bool FP8, bool ROPE>
+__device__ __forceinline__ void fused_append(const DecodeParams& p,
+                                             uint8_t* new_row, int b, int h,
+                                             int page, int slot, int lane, int pos) {
+  const int is_v = lane >> 5;
+  const int c = lane & 31;
+  if (c >= D / 8) return;
+  const uint16_t* src =
+      is_v ? p.v_new + (int64_t)b * p.v_sn + (int64_t)h * p.v_sh
+           : p.k_new + (int64_t)b * p.k_sn + (int64_t)h * p.k_sh;
+  if (ROPE && !is_v) {
+    if (c >= D / 16) return;
+    u32x4 lo = *reinterpret_cast<const u32x4*>(src + 8 * c);
+    u32x4 hi = *reinterpret_cast<const u32x4*>(src + 8 * c + D / 2);
+    float cs[8], sn[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      rope_cos_sin(pos, 8 * c + e, D, p.rope_inv_scale, p.rope_log2_theta, &cs[e], &sn[e]);
+    rope8<BF16>(lo, hi, cs, sn);
+    put_chunk<D, BF16, FP8>(p, new_row, h, page, slot, 0, c, lo);
+    put_chunk<D, BF16, FP8>(p, new_row, h, page, slot, 0, c + D / 16, hi);
+    return;
+  }
+  put_chunk<D, BF16, FP8>(p, new_row, h, page, slot, is_v, c,
+                          *reinterpret_cast<const u32x4*>(src + 8 * c));
+}
+
+template <int D, bool BF16, bool FP8, bool APPEND, bool ROPE>
 __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
@@ -471,16 +498,37 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
         qf[ks] = z;
       }
     }
-
-    // the item that holds the sequence's last page also performs the append
-    int new_pg = -1;  // page index (within the sequence) of the new token
-    const int new_slot = last - 1;
+    int new_pos = npages > 0 ? (npages - 1) * kPage + last - 1 : -1;
     if constexpr (APPEND) {
-      if (npages > 0 && npages - 1 >= page_lo && npages - 1 < page_hi) {
-        const int page = page_id(p, ind_lo, npages - 1, npages);
+      if (p.new_pos) new_pos = uniform(load_invariant(p.new_pos + b));
+    }
+    if constexpr (ROPE) {
+      const int rope_at = new_pos;
+      // d and d + D/2 sit in the same lane: fragments ks and ks + D/64
+#pragma unroll
+      for (int ks = 0; ks < D / 64; ++ks) {
+        float cs[8], sn[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          rope_cos_sin(rope_at, 32 * ks + 8 * G + e, D, p.rope_inv_scale,
+                       p.rope_log2_theta, &cs[e], &sn[e]);
+        rope8<BF16>(qf[ks], qf[ks + D / 64], cs, sn);
+      }
+    }
+
+    // the item that holds the new token's page also performs the append (a
+    // position outside the sequence's pages is skipped, as the stand-alone
+    // append skips it)
+    int new_pg = -1;  // page index (within the sequence) of the new token
+    const int new_slot = new_pos & (kPage - 1);
+    if constexpr (APPEND) {
+      const int pg = new_pos >= 0 ? new_pos / kPage : -1;
+      if (pg >= 0 && pg < npages && pg >= page_lo && pg < page_hi) {
+        const int page = page_id(p, ind_lo, pg, npages);
         if (page >= 0) {
-          new_pg = npages - 1;
-          fused_append<D, BF16, FP8>(p, new_row, b, h, page, new_slot, lane);
+          new_pg = pg;
+          fused_append<D, BF16, FP8, ROPE>(p, new_row, b, h, page, new_slot, lane,
+                                           new_pos);
         }
       }
     }
@@ -618,17 +666,20 @@ __global__ void __launch_bounds__(128)
 using DecodeFn = void (*)(DecodeParams);
 
 template <int D, bool BF16, bool FP8>
-DecodeFn decode_fn(bool append) {
-  return append ? decode_kernel<D, BF16, FP8, true> : decode_kernel<D, BF16, FP8, false>;
+DecodeFn decode_fn(bool append, bool rope) {
+  if (!append) return decode_kernel<D, BF16, FP8, false, false>;
+  return rope ? decode_kernel<D, BF16, FP8, true, true> : decode_kernel<D, BF16, FP8, true, false>;
 }
 
-static DecodeFn pick_decode(int d, bool bf16, bool fp8, bool append) {
+static DecodeFn pick_decode(int d, bool bf16, bool fp8, bool append, bool rope) {
   if (d == 64) {
-    if (bf16) return fp8 ? decode_fn<64, true, true>(append) : decode_fn<64, true, false>(append);
-    return fp8 ? decode_fn<64, false, true>(append) : decode_fn<64, false, false>(append);
+    if (bf16)
+      return fp8 ? decode_fn<64, true, true>(append, rope) : decode_fn<64, true, false>(append, rope);
+    return fp8 ? decode_fn<64, false, true>(append, rope) : decode_fn<64, false, false>(append, rope);
   }
-  if (bf16) return fp8 ? decode_fn<128, true, true>(append) : decode_fn<128, true, false>(append);
-  return fp8 ? decode_fn<128, false, true>(append) : decode_fn<128, false, false>(append);
+  if (bf16)
+    return fp8 ? decode_fn<128, true, true>(append, rope) : decode_fn<128, true, false>(append, rope);
+  return fp8 ? decode_fn<128, false, true>(append, rope) : decode_fn<128, false, false>(append, rope);
 }
 
 // Waves the planner spreads the work over, per CU (one wave per SIMD keeps
@@ -861,6 +912,9 @@ struct AppendRows {
   const void* v;
   int64_t k_sn, k_sh, v_sn, v_sh;
   int32_t dtype;
+  bool rope;
+  const int32_t* new_pos;
+  double rope_inv_scale, rope_log2_theta;
 };
 
 static int decode_run_impl(const char* who, const pagedattn_plan* plan,
@@ -932,10 +986,13 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   p.k_sh = app ? app->k_sh : 0;
   p.v_sn = app ? app->v_sn : 0;
   p.v_sh = app ? app->v_sh : 0;
+  p.new_pos = app ? app->new_pos : nullptr;
+  p.rope_inv_scale = app ? app->rope_inv_scale : 1.0;
+  p.rope_log2_theta = app ? app->rope_log2_theta : 0.0;
 
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = q_dtype == PAGEDATTN_BF16;
-  DecodeFn fn = pick_decode(plan->d, bf16, fp8, app != nullptr);
+  DecodeFn fn = pick_decode(plan->d, bf16, fp8, app != nullptr, app && app->rope);
   const int blocks = ((plan->n_items << plan->hg_shift) + 3) / 4;
   hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, s, p);
   int rc = check_launch(who);
@@ -990,7 +1047,38 @@ int pagedattn_decode_run_append(
                      "are multiples of 8 elements",
                      who);
   AppendRows app{append_key, append_value, k_stride_n, k_stride_h,
-                 v_stride_n, v_stride_h, q_dtype};
+                 v_stride_n, v_stride_h, q_dtype, false, nullptr, 1.0, 0.0};
+  return decode_run_impl(who, plan, q, q_stride_n, q_stride_h, q_dtype,
+                         paged_kv_cache, kv_dtype, kv_scales, num_pages,
+                         kv_indices, num_indices, kv_indptr, kv_last_page_len,
+                         out, lse, sm_scale, &app, stream);
+}
+
+int pagedattn_decode_run_rope_append(
+    const pagedattn_plan* plan, const void* q, int64_t q_stride_n,
+    int64_t q_stride_h, int32_t q_dtype, const void* append_key,
+    const void* append_value, int64_t k_stride_n, int64_t k_stride_h,
+    int64_t v_stride_n, int64_t v_stride_h, const int32_t* positions,
+    float rope_scale, float rope_theta, void* paged_kv_cache, int32_t kv_dtype,
+    const float* kv_scales, int32_t num_pages, const int32_t* kv_indices,
+    int32_t num_indices, const int32_t* kv_indptr,
+    const int32_t* kv_last_page_len, void* out, float* lse, float sm_scale,
+    void* stream) {
+  const char* who = "decode_run_rope_append";
+  if (!append_key || !append_value)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: null append rows", who);
+  if ((k_stride_n & 7) || (k_stride_h & 7) || (v_stride_n & 7) ||
+      (v_stride_h & 7) || !aligned16(append_key) || !aligned16(append_value))
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                     "%s: append rows must be 16-byte aligned with strides that "
+                     "are multiples of 8 elements",
+                     who);
+  if (!(rope_scale > 0.f) || !(rope_theta > 0.f))
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: rope_scale and rope_theta must be > 0",
+                     who);
+  AppendRows app{append_key, append_value, k_stride_n, k_stride_h, v_stride_n,
+                 v_stride_h, q_dtype, true, positions, 1.0 / (double)rope_scale,
+                 std::log2((double)rope_theta)};
   return decode_run_impl(who, plan, q, q_stride_n, q_stride_h, q_dtype,
                          paged_kv_cache, kv_dtype, kv_scales, num_pages,
                          kv_indices, num_indices, kv_indptr, kv_last_page_len,

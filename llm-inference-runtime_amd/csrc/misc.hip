@@ -48,21 +48,17 @@ __global__ void __launch_bounds__(256)
   if (t >= (int64_t)nnz * half) return;
   const int j = (int)(t / half);
   const int i = (int)(t % half);
-  const double inv_freq = exp2(-(double)(2 * i) / (double)rotary_dim * log2_theta);
-  double ang = (double)pos_ids[j] * inv_rope_scale * inv_freq;
-  constexpr double kTwoPi = 6.283185307179586476925286766559;
-  ang -= kTwoPi * rint(ang * (1.0 / kTwoPi));
   float s, c;
-  sincosf((float)ang, &s, &c);
+  rope_cos_sin(pos_ids[j], i, rotary_dim, inv_rope_scale, log2_theta, &c, &s);
   const int i0 = interleave ? 2 * i : i;
   const int i1 = interleave ? 2 * i + 1 : i + half;
   for (int h = 0; h < hq + hkv; ++h) {
     uint16_t* x = h < hq ? q + (int64_t)j * q_sn + (int64_t)h * q_sh
                          : k + (int64_t)j * k_sn + (int64_t)(h - hq) * k_sh;
-    const float x0 = h2f<IS_BF16>(x[i0]);
-    const float x1 = h2f<IS_BF16>(x[i1]);
-    x[i0] = f2h<IS_BF16>(x0 * c - x1 * s);
-    x[i1] = f2h<IS_BF16>(x1 * c + x0 * s);
+    float y0, y1;
+    rope_rotate(h2f<IS_BF16>(x[i0]), h2f<IS_BF16>(x[i1]), c, s, &y0, &y1);
+    x[i0] = f2h<IS_BF16>(y0);
+    x[i1] = f2h<IS_BF16>(y1);
   }
 }
 
@@ -141,6 +137,101 @@ __global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
     o[1] = f32_to_e4m3x4(f[4], f[5], f[6], f[7]);
     *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(a.cache) + dst_elem) = o;
   }
+}
+
+// Writes one 8-element chunk of a K (kind 0) or V (kind 1) row of head h to
+// slot `slot` of `page` (e4m3 pools: quantised with the page's scale).
+template <bool IS_BF16, bool TO_FP8>
+__device__ __forceinline__ void store_chunk(const AppendArgs& a, int64_t page, int slot,
+                                            int kind, int h, int d0, u32x4 x) {
+  const int64_t dst_elem =
+      (((page * 2 + kind) * a.hkv + h) * kPage + slot) * (int64_t)a.d + d0;
+  if constexpr (!TO_FP8) {
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.cache) + dst_elem) = x;
+  } else {
+    const float scale = a.scales[(page * 2 + kind) * a.hkv + h];
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[2 * e] = h2f<IS_BF16>((uint16_t)(x[e] & 0xffffu));
+      f[2 * e + 1] = h2f<IS_BF16>((uint16_t)(x[e] >> 16));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / scale, -448.f), 448.f);
+    u32x2 o;
+    o[0] = f32_to_e4m3x4(f[0], f[1], f[2], f[3]);
+    o[1] = f32_to_e4m3x4(f[4], f[5], f[6], f[7]);
+    *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(a.cache) + dst_elem) = o;
+  }
+}
+
+// ----------------------------------------------------------------------------
+// RoPE + append in one launch: what apply_rope_pos_ids_inplace
+// (src/models/llama.py:175-182, non-interleaved, full head) followed by
+// append_paged_kv_cache (:188-210) do.  Threads [0, nnz * D/16) own (token,
+// frequency chunk of 8): sin/cos once, then every q head rotated in place and
+// every k head rotated in place and written to its page slot.  The remaining
+// threads copy the V rows, one 16-byte chunk each.
+struct RopeAppendArgs {
+  AppendArgs a;
+  uint16_t* q;
+  int64_t q_sn, q_sh;
+  int32_t hq;
+  double inv_scale, log2_theta;
+};
+
+template <bool IS_BF16, bool TO_FP8>
+__global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs r) {
+  const AppendArgs& a = r.a;
+  const int d = a.d;
+  const int nrot = d >> 4;  // frequency chunks of 8 per token
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t n_rot = (int64_t)a.nnz * nrot;
+  if (t < n_rot) {
+    const int j = (int)(t / nrot);
+    const int c = (int)(t % nrot);
+    float cs[8], sn[8];
+    const int pos = a.positions[j];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      rope_cos_sin(pos, 8 * c + e, d, r.inv_scale, r.log2_theta, &cs[e], &sn[e]);
+    for (int h = 0; h < r.hq; ++h) {
+      uint16_t* x = r.q + (int64_t)j * r.q_sn + (int64_t)h * r.q_sh;
+      u32x4 lo = *reinterpret_cast<const u32x4*>(x + 8 * c);
+      u32x4 hi = *reinterpret_cast<const u32x4*>(x + 8 * c + d / 2);
+      rope8<IS_BF16>(lo, hi, cs, sn);
+      *reinterpret_cast<u32x4*>(x + 8 * c) = lo;
+      *reinterpret_cast<u32x4*>(x + 8 * c + d / 2) = hi;
+    }
+    int slot = 0;
+    const int64_t page = append_target_page(a, j, &slot);
+    if (page < 0 && c == 0 && a.err) atomicAdd(a.err, 1);
+    for (int h = 0; h < a.hkv; ++h) {
+      uint16_t* x = const_cast<uint16_t*>(a.k) + (int64_t)j * a.k_sn + (int64_t)h * a.k_sh;
+      u32x4 lo = *reinterpret_cast<const u32x4*>(x + 8 * c);
+      u32x4 hi = *reinterpret_cast<const u32x4*>(x + 8 * c + d / 2);
+      rope8<IS_BF16>(lo, hi, cs, sn);
+      *reinterpret_cast<u32x4*>(x + 8 * c) = lo;
+      *reinterpret_cast<u32x4*>(x + 8 * c + d / 2) = hi;
+      if (page >= 0) {
+        store_chunk<IS_BF16, TO_FP8>(a, page, slot, 0, h, 8 * c, lo);
+        store_chunk<IS_BF16, TO_FP8>(a, page, slot, 0, h, 8 * c + d / 2, hi);
+      }
+    }
+    return;
+  }
+  const int chunks = d >> 3;
+  const int64_t u = t - n_rot;
+  if (u >= (int64_t)a.nnz * a.hkv * chunks) return;
+  const int c = (int)(u % chunks);
+  const int h = (int)((u / chunks) % a.hkv);
+  const int j = (int)(u / ((int64_t)chunks * a.hkv));
+  int slot = 0;
+  const int64_t page = append_target_page(a, j, &slot);
+  if (page < 0) return;
+  const u32x4 x = *reinterpret_cast<const u32x4*>(a.v + (int64_t)j * a.v_sn +
+                                                  (int64_t)h * a.v_sh + 8 * c);
+  store_chunk<IS_BF16, TO_FP8>(a, page, slot, 1, h, 8 * c, x);
 }
 
 // ----------------------------------------------------------------------------
@@ -277,6 +368,80 @@ int pagedattn_apply_rope_pos_ids_inplace(
   return check_launch("apply_rope_pos_ids_inplace");
 }
 
+}  // extern "C"
+
+namespace pa {
+
+// Validation and argument packing shared by the append entry points.
+// Returns PAGEDATTN_OK with *a filled, or an error; *empty is set when there
+// is nothing to do (nnz == 0).
+static int append_setup(const char* who, const void* append_key, const void* append_value,
+                        int64_t k_stride_n, int64_t k_stride_h, int64_t v_stride_n,
+                        int64_t v_stride_h, int32_t src_dtype, const int32_t* batch_indices,
+                        const int32_t* positions, int32_t nnz, void* paged_kv_cache,
+                        int32_t cache_dtype, const float* kv_scales, int32_t num_pages,
+                        const int32_t* kv_indices, int32_t num_indices,
+                        const int32_t* kv_indptr, int32_t batch_size, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t page_size, int32_t* error_flag,
+                        AppendArgs* a, bool* empty) {
+  *empty = false;
+  if (page_size != kPage)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: page_size %d not supported (16)", who,
+                     page_size);
+  if (src_dtype != PAGEDATTN_BF16 && src_dtype != PAGEDATTN_F16)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: source dtype %d not supported", who,
+                     src_dtype);
+  if (cache_dtype != src_dtype && cache_dtype != PAGEDATTN_E4M3)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                     "%s: cache dtype %d must equal the source dtype %d or be e4m3", who,
+                     cache_dtype, src_dtype);
+  if (cache_dtype == PAGEDATTN_E4M3 && !kv_scales)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: e4m3 cache needs kv_scales", who);
+  if (nnz < 0 || batch_size < 0 || num_pages < 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      (head_dim & 7))
+    return set_error(PAGEDATTN_ERR_INVALID,
+                     "%s: bad shape nnz=%d batch=%d pages=%d hkv=%d d=%d (d must be a "
+                     "multiple of 8)",
+                     who, nnz, batch_size, num_pages, num_kv_heads, head_dim);
+  if ((k_stride_n & 7) || (k_stride_h & 7) || (v_stride_n & 7) || (v_stride_h & 7) ||
+      !aligned16(append_key) || !aligned16(append_value) || !aligned16(paged_kv_cache))
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                     "%s: k/v/cache must be 16-byte aligned with strides that are "
+                     "multiples of 8 elements",
+                     who);
+  if (nnz == 0) {
+    *empty = true;
+    return PAGEDATTN_OK;
+  }
+  if (!append_key || !append_value || !batch_indices || !positions || !paged_kv_cache ||
+      !kv_indices || !kv_indptr)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: null pointer", who);
+  a->k = (const uint16_t*)append_key;
+  a->v = (const uint16_t*)append_value;
+  a->k_sn = k_stride_n;
+  a->k_sh = k_stride_h;
+  a->v_sn = v_stride_n;
+  a->v_sh = v_stride_h;
+  a->batch_indices = batch_indices;
+  a->positions = positions;
+  a->nnz = nnz;
+  a->cache = paged_kv_cache;
+  a->scales = kv_scales;
+  a->num_pages = num_pages;
+  a->kv_indices = kv_indices;
+  a->num_indices = num_indices;
+  a->kv_indptr = kv_indptr;
+  a->batch_size = batch_size;
+  a->hkv = num_kv_heads;
+  a->d = head_dim;
+  a->err = error_flag;
+  return PAGEDATTN_OK;
+}
+
+}  // namespace pa
+
+extern "C" {
+
 int pagedattn_append_paged_kv_cache(
     const void* append_key, const void* append_value, int64_t k_stride_n,
     int64_t k_stride_h, int64_t v_stride_n, int64_t v_stride_h,
@@ -287,59 +452,14 @@ int pagedattn_append_paged_kv_cache(
     const int32_t* kv_last_page_len, int32_t batch_size, int32_t num_kv_heads,
     int32_t head_dim, int32_t page_size, int32_t* error_flag, void* stream) {
   (void)kv_last_page_len;  // not used for addressing, as in the reference
-  if (page_size != kPage)
-    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
-                     "append_paged_kv_cache: page_size %d not supported (16)",
-                     page_size);
-  if (src_dtype != PAGEDATTN_BF16 && src_dtype != PAGEDATTN_F16)
-    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
-                     "append_paged_kv_cache: source dtype %d not supported",
-                     src_dtype);
-  if (cache_dtype != src_dtype && cache_dtype != PAGEDATTN_E4M3)
-    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
-                     "append_paged_kv_cache: cache dtype %d must equal the "
-                     "source dtype %d or be e4m3",
-                     cache_dtype, src_dtype);
-  if (cache_dtype == PAGEDATTN_E4M3 && !kv_scales)
-    return set_error(PAGEDATTN_ERR_INVALID,
-                     "append_paged_kv_cache: e4m3 cache needs kv_scales");
-  if (nnz < 0 || batch_size < 0 || num_pages < 0 || num_kv_heads <= 0 ||
-      head_dim <= 0 || (head_dim & 7))
-    return set_error(PAGEDATTN_ERR_INVALID,
-                     "append_paged_kv_cache: bad shape nnz=%d batch=%d "
-                     "pages=%d hkv=%d d=%d (d must be a multiple of 8)",
-                     nnz, batch_size, num_pages, num_kv_heads, head_dim);
-  if ((k_stride_n & 7) || (k_stride_h & 7) || (v_stride_n & 7) ||
-      (v_stride_h & 7) || !aligned16(append_key) || !aligned16(append_value) ||
-      !aligned16(paged_kv_cache))
-    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
-                     "append_paged_kv_cache: k/v/cache must be 16-byte aligned "
-                     "with strides that are multiples of 8 elements");
-  if (nnz == 0) return PAGEDATTN_OK;
-  if (!append_key || !append_value || !batch_indices || !positions ||
-      !paged_kv_cache || !kv_indices || !kv_indptr)
-    return set_error(PAGEDATTN_ERR_INVALID,
-                     "append_paged_kv_cache: null pointer");
   AppendArgs a;
-  a.k = (const uint16_t*)append_key;
-  a.v = (const uint16_t*)append_value;
-  a.k_sn = k_stride_n;
-  a.k_sh = k_stride_h;
-  a.v_sn = v_stride_n;
-  a.v_sh = v_stride_h;
-  a.batch_indices = batch_indices;
-  a.positions = positions;
-  a.nnz = nnz;
-  a.cache = paged_kv_cache;
-  a.scales = kv_scales;
-  a.num_pages = num_pages;
-  a.kv_indices = kv_indices;
-  a.num_indices = num_indices;
-  a.kv_indptr = kv_indptr;
-  a.batch_size = batch_size;
-  a.hkv = num_kv_heads;
-  a.d = head_dim;
-  a.err = error_flag;
+  bool empty = false;
+  int rc = append_setup("append_paged_kv_cache", append_key, append_value, k_stride_n,
+                        k_stride_h, v_stride_n, v_stride_h, src_dtype, batch_indices,
+                        positions, nnz, paged_kv_cache, cache_dtype, kv_scales, num_pages,
+                        kv_indices, num_indices, kv_indptr, batch_size, num_kv_heads,
+                        head_dim, page_size, error_flag, &a, &empty);
+  if (rc || empty) return rc;
   const int64_t threads = (int64_t)nnz * 2 * num_kv_heads * (head_dim / 8);
   const dim3 grid((unsigned)((threads + 255) / 256));
   hipStream_t s = (hipStream_t)stream;
@@ -350,6 +470,63 @@ int pagedattn_append_paged_kv_cache(
   else
     hipLaunchKernelGGL((append_kernel<false, true>), grid, dim3(256), 0, s, a);
   return check_launch("append_paged_kv_cache");
+}
+
+int pagedattn_rope_append_paged_kv_cache(
+    void* q, int64_t q_stride_n, int64_t q_stride_h, int32_t num_qo_heads,
+    void* append_key, const void* append_value, int64_t k_stride_n,
+    int64_t k_stride_h, int64_t v_stride_n, int64_t v_stride_h,
+    int32_t src_dtype, const int32_t* batch_indices, const int32_t* positions,
+    int32_t nnz, float rope_scale, float rope_theta, void* paged_kv_cache,
+    int32_t cache_dtype, const float* kv_scales, int32_t num_pages,
+    const int32_t* kv_indices, int32_t num_indices, const int32_t* kv_indptr,
+    int32_t batch_size, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+    int32_t* error_flag, void* stream) {
+  const char* who = "rope_append_paged_kv_cache";
+  if (!(rope_scale > 0.f) || !(rope_theta > 0.f))
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: rope_scale and rope_theta must be > 0",
+                     who);
+  if (num_qo_heads < 0 || (head_dim & 15))
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: bad shape hq=%d d=%d (d must be a "
+                     "multiple of 16)", who, num_qo_heads, head_dim);
+  if ((q_stride_n & 7) || (q_stride_h & 7) || !aligned16(q))
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                     "%s: q must be 16-byte aligned with strides that are multiples "
+                     "of 8 elements", who);
+  AppendArgs a;
+  bool empty = false;
+  int rc = append_setup(who, append_key, append_value, k_stride_n, k_stride_h, v_stride_n,
+                        v_stride_h, src_dtype, batch_indices, positions, nnz, paged_kv_cache,
+                        cache_dtype, kv_scales, num_pages, kv_indices, num_indices, kv_indptr,
+                        batch_size, num_kv_heads, head_dim, page_size, error_flag, &a, &empty);
+  if (rc || empty) return rc;
+  if (num_qo_heads > 0 && !q)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: null q", who);
+  RopeAppendArgs r;
+  r.a = a;
+  r.q = static_cast<uint16_t*>(q);
+  r.q_sn = q_stride_n;
+  r.q_sh = q_stride_h;
+  r.hq = num_qo_heads;
+  r.inv_scale = 1.0 / (double)rope_scale;
+  r.log2_theta = std::log2((double)rope_theta);
+  const int64_t threads = (int64_t)nnz * (head_dim / 16) +
+                          (int64_t)nnz * num_kv_heads * (head_dim / 8);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  hipStream_t s = (hipStream_t)stream;
+  const bool bf16 = src_dtype == PAGEDATTN_BF16;
+  if (cache_dtype != PAGEDATTN_E4M3) {
+    if (bf16)
+      hipLaunchKernelGGL((rope_append_kernel<true, false>), grid, dim3(256), 0, s, r);
+    else
+      hipLaunchKernelGGL((rope_append_kernel<false, false>), grid, dim3(256), 0, s, r);
+  } else {
+    if (bf16)
+      hipLaunchKernelGGL((rope_append_kernel<true, true>), grid, dim3(256), 0, s, r);
+    else
+      hipLaunchKernelGGL((rope_append_kernel<false, true>), grid, dim3(256), 0, s, r);
+  }
+  return check_launch(who);
 }
 
 int pagedattn_quantize_pages_e4m3(const void* src_cache, int32_t src_dtype,

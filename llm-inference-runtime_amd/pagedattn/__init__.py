@@ -15,6 +15,7 @@ from .ops import (  # noqa: F401
     copy_bytes,
     get_batch_indices_positions,
     quantize_pages_e4m3,
+    rope_append_paged_kv_cache,
 )
 from ._lib import LIB_PATH, PagedAttnError, lib  # noqa: F401
 
@@ -27,6 +28,7 @@ __all__ = [
     "copy_bytes",
     "get_batch_indices_positions",
     "quantize_pages_e4m3",
+    "rope_append_paged_kv_cache",
     "LIB_PATH",
     "PagedAttnError",
     "lib",

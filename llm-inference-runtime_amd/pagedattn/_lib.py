@@ -57,6 +57,11 @@ _SIGNATURES = {
         [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p,
          _c_int, _c_p, _c_int, _c_p, _c_int, _c_p, _c_int, _c_p, _c_p,
          _c_int, _c_int, _c_int, _c_int, _c_p, _c_p]),
+    "pagedattn_rope_append_paged_kv_cache": (
+        _c_int,
+        [_c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
+         _c_p, _c_p, _c_int, _c_f, _c_f, _c_p, _c_int, _c_p, _c_int, _c_p, _c_int, _c_p,
+         _c_int, _c_int, _c_int, _c_int, _c_p, _c_p]),
     "pagedattn_plan_create": (_c_p, []),
     "pagedattn_plan_destroy": (None, [_c_p]),
     "pagedattn_decode_plan": (
@@ -71,6 +76,11 @@ _SIGNATURES = {
         _c_int,
         [_c_p, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
          _c_p, _c_int, _c_p, _c_int, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p, _c_f, _c_p]),
+    "pagedattn_decode_run_rope_append": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64,
+         _c_p, _c_f, _c_f, _c_p, _c_int, _c_p, _c_int, _c_p, _c_int, _c_p, _c_p, _c_p, _c_p,
+         _c_f, _c_p]),
     "pagedattn_prefill_plan": (
         _c_int,
         [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_int,

@@ -28,6 +28,11 @@ from torch import nn
 from . import ops
 
 
+# Fused launches on the engine's hot path: RoPE + append (+ decode attention)
+# in one kernel each.  False runs the three reference calls separately.
+FUSE = True
+
+
 class FlashInferState:
     """Process-global state shared by all layers of one forward
     (src/models/llama.py:16-36).  Attributes are writable from outside: the
@@ -137,22 +142,41 @@ def patched_llama_attention_forward(self, hidden_states: torch.Tensor,
     v_rows = v.view(-1, self.num_key_value_heads, self.head_dim)
 
     positions = cast(torch.Tensor, FlashInferState.positions)
-    ops.apply_rope_pos_ids_inplace(q_rows, k_rows, positions, rope_theta=self.rope_theta,
-                                   rope_scale=self.rope_scale, interleave=False)
-
     pool = cast(torch.Tensor, FlashInferState.kv_pool)
     layer_pool = pool[self.layer_idx]
     scales = FlashInferState.kv_scales
     layer_scales = scales[self.layer_idx] if scales is not None else None
     ws = cast(torch.Tensor, FlashInferState.workspace_buffer)
-    ops.append_paged_kv_cache(
-        k_rows, v_rows, cast(torch.Tensor, FlashInferState.batch_indices), positions,
-        layer_pool, cast(torch.Tensor, FlashInferState.kv_indices),
-        cast(torch.Tensor, FlashInferState.kv_indptr),
-        cast(torch.Tensor, FlashInferState.kv_last_page_len), kv_layout="HND",
-        kv_scales=layer_scales, error_flag=ws[:4].view(torch.int32))
+    decode = FlashInferState.mode != "prefill"
 
-    if FlashInferState.mode == "prefill":
+    if FUSE and decode and _decode_rows_match(q_rows):
+        # RoPE + append + attention of the decode step in one launch
+        dw = cast(ops.BatchDecodeWithPagedKVCacheWrapper, FlashInferState.decode_wrapper)
+        out = dw.run(q_rows, layer_pool, kv_scales=layer_scales, append_key=k_rows,
+                     append_value=v_rows, rope=(self.rope_scale, self.rope_theta),
+                     positions=positions)
+        return self.o_proj(out.reshape(bsz, 1, self.num_heads * self.head_dim)), None
+
+    if FUSE:
+        # RoPE + append in one launch, then attention
+        ops.rope_append_paged_kv_cache(
+            q_rows, k_rows, v_rows, cast(torch.Tensor, FlashInferState.batch_indices),
+            positions, layer_pool, cast(torch.Tensor, FlashInferState.kv_indices),
+            cast(torch.Tensor, FlashInferState.kv_indptr),
+            cast(torch.Tensor, FlashInferState.kv_last_page_len), kv_layout="HND",
+            rope_scale=self.rope_scale, rope_theta=self.rope_theta, kv_scales=layer_scales,
+            error_flag=ws[:4].view(torch.int32))
+    else:
+        ops.apply_rope_pos_ids_inplace(q_rows, k_rows, positions, rope_theta=self.rope_theta,
+                                       rope_scale=self.rope_scale, interleave=False)
+        ops.append_paged_kv_cache(
+            k_rows, v_rows, cast(torch.Tensor, FlashInferState.batch_indices), positions,
+            layer_pool, cast(torch.Tensor, FlashInferState.kv_indices),
+            cast(torch.Tensor, FlashInferState.kv_indptr),
+            cast(torch.Tensor, FlashInferState.kv_last_page_len), kv_layout="HND",
+            kv_scales=layer_scales, error_flag=ws[:4].view(torch.int32))
+
+    if not decode:
         pw = cast(ops.BatchPrefillWithPagedKVCacheWrapper, FlashInferState.prefill_wrapper)
         out = pw.forward(q_rows, layer_pool, causal=True, kv_scales=layer_scales)
         out = out.reshape(bsz, q_len, self.num_heads * self.head_dim)
@@ -161,6 +185,15 @@ def patched_llama_attention_forward(self, hidden_states: torch.Tensor,
         out = dw.forward(q_rows, layer_pool, kv_scales=layer_scales)
         out = out.reshape(bsz, 1, self.num_heads * self.head_dim)
     return self.o_proj(out), None
+
+
+def _decode_rows_match(q_rows: torch.Tensor) -> bool:
+    """The fused decode launch appends row b at kv_len_b - 1: it applies when
+    the step carries exactly one new token per planned sequence, laid out in
+    sequence order (batch_indices = arange(B)), as the engine's decode step
+    does (step_executor.py:204-234)."""
+    dw = cast(ops.BatchDecodeWithPagedKVCacheWrapper, FlashInferState.decode_wrapper)
+    return q_rows.shape[0] == getattr(dw, "_bsz", -1)
 
 
 def _fuse_qkv_proj(attn) -> nn.Linear:

@@ -190,6 +190,48 @@ def append_paged_kv_cache(append_key: torch.Tensor, append_value: torch.Tensor,
          ptr(error_flag), _stream(device))
 
 
+def rope_append_paged_kv_cache(q: torch.Tensor, append_key: torch.Tensor,
+                               append_value: torch.Tensor, batch_indices: torch.Tensor,
+                               positions: torch.Tensor, paged_kv_cache: torch.Tensor,
+                               kv_indices: torch.Tensor, kv_indptr: torch.Tensor,
+                               kv_last_page_len: torch.Tensor, kv_layout: str = "NHD",
+                               rope_scale: float = 1.0, rope_theta: float = 1e4,
+                               kv_scales: torch.Tensor | None = None,
+                               error_flag: torch.Tensor | None = None) -> None:
+    """apply_rope_pos_ids_inplace(q, append_key, positions, interleave=False)
+    followed by append_paged_kv_cache(...) in one launch
+    (src/models/llama.py:175-210): q and append_key are rotated in place, the
+    rotated K rows and the V rows land in their pages.  Same results as the
+    two calls."""
+    num_pages, hkv, d = _check_pool(paged_kv_cache, None, None, kv_layout)
+    _check_rows(q, "q", None, d)
+    _check_rows(append_key, "append_key", hkv, d)
+    _check_rows(append_value, "append_value", hkv, d)
+    if not (q.dtype == append_key.dtype == append_value.dtype):
+        raise ValueError("q, append_key and append_value must share a dtype")
+    nnz = append_key.shape[0]
+    if (q.shape[0] != nnz or append_value.shape[0] != nnz or batch_indices.numel() != nnz
+            or positions.numel() != nnz):
+        raise ValueError("q, append_key/value, batch_indices and positions disagree on nnz")
+    scales = _check_scales(kv_scales, paged_kv_cache)
+    if paged_kv_cache.dtype not in (append_key.dtype, torch.float8_e4m3fn):
+        raise ValueError(f"pool dtype {paged_kv_cache.dtype} cannot take {append_key.dtype} rows")
+    device = paged_kv_cache.device
+    bi = _i32(batch_indices, device)
+    pos = _i32(positions, device)
+    ind = _i32(kv_indices, device)
+    indptr = _i32(kv_indptr, device)
+    bsz = indptr.numel() - 1
+    if error_flag is not None and (error_flag.dtype != torch.int32 or error_flag.numel() < 1):
+        raise ValueError("error_flag must be an int32 device tensor")
+    call("pagedattn_rope_append_paged_kv_cache", ptr(q), q.stride(0), q.stride(1), q.shape[1],
+         ptr(append_key), ptr(append_value), append_key.stride(0), append_key.stride(1),
+         append_value.stride(0), append_value.stride(1), dtype_code(append_key.dtype), ptr(bi),
+         ptr(pos), nnz, float(rope_scale), float(rope_theta), ptr(paged_kv_cache),
+         dtype_code(paged_kv_cache.dtype), ptr(scales), num_pages, ptr(ind), ind.numel(),
+         ptr(indptr), bsz, hkv, d, PAGE_SIZE, ptr(error_flag), _stream(device))
+
+
 def quantize_pages_e4m3(pool: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """bf16/fp16 layer pool -> (e4m3 pool, fp32 scales [P, 2, Hkv]) with
     scale = amax / 448 per (page, K|V, kv-head) block (1.0 for an all-zero block)."""
@@ -312,11 +354,16 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
             kv_scales: torch.Tensor | None = None, out: torch.Tensor | None = None,
             lse: torch.Tensor | None = None, return_lse: bool = False,
             sm_scale: float | None = None, append_key: torch.Tensor | None = None,
-            append_value: torch.Tensor | None = None):
+            append_value: torch.Tensor | None = None, rope: tuple[float, float] | None = None,
+            positions: torch.Tensor | None = None):
         """Decode attention.  With append_key/append_value ([B, Hkv, D], the
         newest token of every sequence, position kv_len - 1) the page append
         of the decode step runs inside the same launch (the engine's decode
-        step: batch_indices = arange(B), positions = kv_len - 1)."""
+        step: batch_indices = arange(B), positions = kv_len - 1).  With
+        rope=(rope_scale, rope_theta) as well, q and append_key are rotated
+        (non-interleaved RoPE at `positions`, default kv_len - 1) inside that
+        launch too: apply_rope_pos_ids_inplace + append + attention in one
+        kernel (q and append_key themselves are left unrotated)."""
         if not self._planned:
             raise RuntimeError("plan()/begin_forward() must be called before run()/forward()")
         num_pages, _, _ = _check_pool(paged_kv_cache, self._hkv, self._d, self._kv_layout)
@@ -348,10 +395,25 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
                 _check_rows(t, name, self._hkv, self._d)
                 if t.shape[0] != self._bsz or t.dtype != q.dtype:
                     raise ValueError(f"{name} must be [batch, num_kv_heads, head_dim] in q's dtype")
-            call("pagedattn_decode_run_append", self._plan.handle, ptr(q), q.stride(0),
-                 q.stride(1), dtype_code(q.dtype), ptr(append_key), ptr(append_value),
-                 append_key.stride(0), append_key.stride(1), append_value.stride(0),
-                 append_value.stride(1), *common)
+            if rope is None:
+                if positions is not None:
+                    raise ValueError("positions only applies together with rope")
+                call("pagedattn_decode_run_append", self._plan.handle, ptr(q), q.stride(0),
+                     q.stride(1), dtype_code(q.dtype), ptr(append_key), ptr(append_value),
+                     append_key.stride(0), append_key.stride(1), append_value.stride(0),
+                     append_value.stride(1), *common)
+            else:
+                rope_scale, rope_theta = rope
+                pos = None
+                if positions is not None:
+                    if positions.numel() != self._bsz:
+                        raise ValueError("positions must hold one entry per sequence")
+                    pos = _i32(positions, q.device)
+                call("pagedattn_decode_run_rope_append", self._plan.handle, ptr(q),
+                     q.stride(0), q.stride(1), dtype_code(q.dtype), ptr(append_key),
+                     ptr(append_value), append_key.stride(0), append_key.stride(1),
+                     append_value.stride(0), append_value.stride(1), ptr(pos),
+                     float(rope_scale), float(rope_theta), *common)
         return (out, lse) if return_lse else out
 
     def forward(self, q: torch.Tensor, paged_kv_cache: torch.Tensor,

@@ -227,3 +227,56 @@ def test_decode_fused_append_tinyllama_at_scale(gpu):
     assert np.array_equal(O.to_bits(t.pool), want)
     ref_o, _ = oracle_decode(m, t.pool, t.q)
     assert max_err(out, ref_o) <= TOL_BF16
+
+
+@pytest.mark.parametrize("d,hq,hkv,fp8", [(64, 32, 4, False), (128, 32, 8, False),
+                                          (128, 64, 8, True)])
+def test_decode_rope_append_equals_separate(gpu, d, hq, hkv, fp8):
+    # one launch (RoPE of q and the new K row + append + attention) ==
+    # apply_rope_pos_ids_inplace, append_paged_kv_cache, decode: bit for bit
+    meta, pool, q = decode_case(gpu, EDGE_LENS, hq, hkv, d, seed=41)
+    bsz = len(EDGE_LENS)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(42)
+    kn = torch.randn((bsz, hkv, d), generator=g, device=gpu).to(torch.bfloat16) * 3
+    vn = torch.randn((bsz, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+    scales = None
+    if fp8:
+        pool, scales = pagedattn.quantize_pages_e4m3(pool)
+    lens = np.asarray(EDGE_LENS, dtype=np.int64)
+    rng = np.random.default_rng(43)
+    # the engine's positions (kv_len - 1) and arbitrary earlier positions
+    for pos in (lens - 1, rng.integers(0, lens)):
+        ws = workspace(gpu)
+        for split in (0, 8):
+            w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+            w.plan(i32(meta.kv_indptr, gpu), i32(meta.kv_indices, gpu),
+                   i32(meta.kv_last_page_len, gpu), hq, hkv, d, 16,
+                   q_data_type=torch.bfloat16, split_pages=split)
+            pa_, qa, ka = pool.clone(), q.clone(), kn.clone()
+            pagedattn.apply_rope_pos_ids_inplace(qa, ka, i32(pos, gpu), rope_theta=10000.0,
+                                                 rope_scale=1.0)
+            pagedattn.append_paged_kv_cache(ka, vn, i32(np.arange(bsz), gpu), i32(pos, gpu),
+                                            pa_, i32(meta.kv_indices, gpu),
+                                            i32(meta.kv_indptr, gpu),
+                                            i32(meta.kv_last_page_len, gpu), kv_layout="HND",
+                                            kv_scales=scales)
+            o_sep, l_sep = w.run(qa, pa_, kv_scales=scales, return_lse=True)
+            pb_ = pool.clone()
+            o_fus, l_fus = w.run(q, pb_, kv_scales=scales, return_lse=True, append_key=kn,
+                                 append_value=vn, rope=(1.0, 10000.0),
+                                 positions=i32(pos, gpu))
+            torch.cuda.synchronize()
+            assert np.array_equal(O.to_bits(pa_), O.to_bits(pb_)), split
+            assert torch.equal(o_sep, o_fus), split
+            assert torch.equal(l_sep, l_fus), split
+    # positions omitted means kv_len - 1
+    pc_ = pool.clone()
+    o_def = w.run(q, pc_, kv_scales=scales, append_key=kn, append_value=vn,
+                  rope=(1.0, 10000.0))
+    pd_ = pool.clone()
+    o_exp = w.run(q, pd_, kv_scales=scales, append_key=kn, append_value=vn,
+                  rope=(1.0, 10000.0), positions=i32(lens - 1, gpu))
+    torch.cuda.synchronize()
+    assert torch.equal(o_def, o_exp)
+    assert np.array_equal(O.to_bits(pc_), O.to_bits(pd_))

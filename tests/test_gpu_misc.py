@@ -158,3 +158,41 @@ def test_rope(gpu, dtype, theta, scale, interleave):
     tolk = (_bf16_ulp(rk) if dtype == torch.bfloat16 else rk.abs() * 2.0 ** -10) + 1e-5
     assert bool(((k.float().cpu() - rk).abs() <= tolk).all())
     assert torch.equal(qkv[:, (hq + hkv) * d:], v_before)  # v untouched
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("prefill", [False, True])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_rope_append_equals_separate(gpu, dtype, prefill, fp8):
+    # one launch == apply_rope_pos_ids_inplace then append_paged_kv_cache,
+    # bit for bit: rotated q and k in place and the pool
+    meta, pool, k, v = _append_case(gpu, dtype, 5, prefill)
+    hq = 8
+    g = torch.Generator(device=gpu)
+    g.manual_seed(6)
+    q = strided_rows(meta.nnz, hq, pool.shape[-1], dtype, gpu, g, lead=0, tail=8)
+    scales = None
+    if fp8:
+        pool, scales = pagedattn.quantize_pages_e4m3(pool)
+    pos = meta.positions.copy()
+    bi = meta.batch_indices.copy()
+    bi[0] = 1000  # a token the append must skip (and count); RoPE still rotates it
+    args = dict(kv_layout="HND", kv_scales=scales)
+    q_a, k_a, pool_a = q.clone(), k.clone(), pool.clone()
+    err_a = torch.zeros(1, dtype=torch.int32, device=gpu)
+    pagedattn.apply_rope_pos_ids_inplace(q_a, k_a, i32(pos, gpu), rope_theta=500000.0,
+                                         rope_scale=2.0)
+    pagedattn.append_paged_kv_cache(k_a, v, i32(bi, gpu), i32(pos, gpu), pool_a,
+                                    i32(meta.kv_indices, gpu), i32(meta.kv_indptr, gpu),
+                                    i32(meta.kv_last_page_len, gpu), error_flag=err_a, **args)
+    q_b, k_b, pool_b = q.clone(), k.clone(), pool.clone()
+    err_b = torch.zeros(1, dtype=torch.int32, device=gpu)
+    pagedattn.rope_append_paged_kv_cache(q_b, k_b, v, i32(bi, gpu), i32(pos, gpu), pool_b,
+                                         i32(meta.kv_indices, gpu), i32(meta.kv_indptr, gpu),
+                                         i32(meta.kv_last_page_len, gpu), rope_scale=2.0,
+                                         rope_theta=500000.0, error_flag=err_b, **args)
+    torch.cuda.synchronize()
+    assert torch.equal(q_a, q_b)
+    assert torch.equal(k_a, k_b)
+    assert np.array_equal(O.to_bits(pool_a), O.to_bits(pool_b))
+    assert int(err_a.item()) == int(err_b.item()) == 1
