@@ -146,6 +146,52 @@ int pagedattn_rope_append_paged_kv_cache(
     int32_t batch_size, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
     int32_t* error_flag, void* stream);
 
+/* e4m3 append that maintains the page scales (no reference counterpart: the
+ * engine's fp8 write path; the reference pool dtype is the model dtype,
+ * src/engine/memory/allocator.py:34).  Same metadata, strides and error
+ * contract as pagedattn_append_paged_kv_cache into an E4M3 cache.
+ * A run = tokens of one sequence that land in one page, consecutive and in
+ * position order in the token list (what get_batch_indices_positions
+ * produces).  For each run and each (K|V, kv-head) block, with slot0 the
+ * run's first slot and s = kv_scales[(page*2 + {0,1})*num_kv_heads + h]:
+ *   s_old = slot0 > 0 ? s : 0
+ *   s_new = max(s_old, smallest power of two p with 448 * p >= amax(run rows))
+ *   if s_new > s_old: rows [0, slot0) are re-encoded as
+ *       round(clamp(decode(row) * (s_old / s_new), +-448))
+ *   run rows = round(clamp(x / s_new, +-448)), zero codes when s_new == 0
+ *   s = s_new
+ * (round = to nearest even e4m3fn).  kv_scales is read and written.  Two
+ * runs that write one page in the same call race; the caller forks shared
+ * pages first (pagedattn_fork_pages).  head_dim <= 256, multiple of 8. */
+int pagedattn_append_paged_kv_cache_e4m3_amax(
+    const void* append_key, const void* append_value, int64_t k_stride_n,
+    int64_t k_stride_h, int64_t v_stride_n, int64_t v_stride_h, int32_t src_dtype,
+    const int32_t* batch_indices, const int32_t* positions, int32_t nnz,
+    void* paged_kv_cache, float* kv_scales, int32_t num_pages, const int32_t* kv_indices,
+    int32_t num_indices, const int32_t* kv_indptr, int32_t batch_size,
+    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int32_t* error_flag,
+    void* stream);
+
+/* Copy-on-write page fork over the whole pool (no FlashInfer counterpart; the
+ * copy step of the reference's todo.md:17-19 "Copy-on-Write" item, for pages
+ * shared through src/engine/memory/radix_cache.py:60-88).  kv_pool is the
+ * engine's contiguous [num_layers, num_pages, 2, num_kv_heads, page_size,
+ * head_dim] array of pool_dtype (F16, BF16 or E4M3; head_dim * element size a
+ * multiple of 16 bytes).  For fork f and every layer l, rows
+ * [0, valid_tokens[f]) (all page_size rows when valid_tokens is NULL) of
+ * every (K|V, kv-head) block of page src_pages[f] are copied to page
+ * dst_pages[f]; for E4M3 the kv_scales [num_layers, num_pages, 2,
+ * num_kv_heads] entries are copied too (kv_scales may be NULL otherwise).
+ * src/dst/valid are device int32 arrays of num_forks entries; a fork with a
+ * page outside [0, num_pages) or a count outside [0, page_size] is skipped
+ * and counted in *error_flag; src == dst is a no-op.  Destinations must be
+ * distinct and must not be sources of the same call. */
+int pagedattn_fork_pages(void* kv_pool, int32_t pool_dtype, int32_t num_layers,
+                         int32_t num_pages, int32_t num_kv_heads, int32_t head_dim,
+                         int32_t page_size, float* kv_scales, const int32_t* src_pages,
+                         const int32_t* dst_pages, const int32_t* valid_tokens,
+                         int32_t num_forks, int32_t* error_flag, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Plans.  pagedattn_plan_create/destroy manage the host object.
  * BatchDecodeWithPagedKVCacheWrapper.begin_forward(kv_indptr, kv_indices,

@@ -11,8 +11,10 @@ from .ops import (  # noqa: F401
     BatchDecodeWithPagedKVCacheWrapper,
     BatchPrefillWithPagedKVCacheWrapper,
     append_paged_kv_cache,
+    append_paged_kv_cache_e4m3_amax,
     apply_rope_pos_ids_inplace,
     copy_bytes,
+    fork_pages,
     get_batch_indices_positions,
     quantize_pages_e4m3,
     rope_append_paged_kv_cache,
@@ -24,8 +26,10 @@ __all__ = [
     "BatchDecodeWithPagedKVCacheWrapper",
     "BatchPrefillWithPagedKVCacheWrapper",
     "append_paged_kv_cache",
+    "append_paged_kv_cache_e4m3_amax",
     "apply_rope_pos_ids_inplace",
     "copy_bytes",
+    "fork_pages",
     "get_batch_indices_positions",
     "quantize_pages_e4m3",
     "rope_append_paged_kv_cache",

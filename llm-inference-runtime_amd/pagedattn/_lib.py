@@ -62,6 +62,14 @@ _SIGNATURES = {
         [_c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int,
          _c_p, _c_p, _c_int, _c_f, _c_f, _c_p, _c_int, _c_p, _c_int, _c_p, _c_int, _c_p,
          _c_int, _c_int, _c_int, _c_int, _c_p, _c_p]),
+    "pagedattn_append_paged_kv_cache_e4m3_amax": (
+        _c_int,
+        [_c_p, _c_p, _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_int, _c_p, _c_p,
+         _c_int, _c_p, _c_int, _c_p, _c_int, _c_int, _c_int, _c_int, _c_p, _c_p]),
+    "pagedattn_fork_pages": (
+        _c_int,
+        [_c_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_p, _c_p, _c_p, _c_p, _c_int,
+         _c_p, _c_p]),
     "pagedattn_plan_create": (_c_p, []),
     "pagedattn_plan_destroy": (None, [_c_p]),
     "pagedattn_decode_plan": (

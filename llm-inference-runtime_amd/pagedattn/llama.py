@@ -16,6 +16,10 @@ Deliberate differences from the reference:
 * bitsandbytes 4-bit projections (src/models/llama.py:283-336) are not fused
   (bitsandbytes is CUDA-only); such a model raises NotImplementedError.
 * The pool may be e4m3 with ``FlashInferState.kv_scales`` [L, P, 2, Hkv].
+  With ``kv_scale_policy == "running"`` (the default) every append keeps
+  the scales of the pages it writes a running amax
+  (``append_paged_kv_cache_e4m3_amax``); ``"fixed"`` encodes with the scales
+  as given (pools quantised ahead of time).
 """
 
 from __future__ import annotations
@@ -41,6 +45,7 @@ class FlashInferState:
 
     kv_pool: torch.Tensor | None = None
     kv_scales: torch.Tensor | None = None  # e4m3 pools only: [L, P, 2, Hkv]
+    kv_scale_policy: str = "running"  # e4m3 pools: "running" amax or "fixed" scales
 
     kv_indices: torch.Tensor | None = None
     kv_indptr: torch.Tensor | None = None
@@ -64,13 +69,17 @@ WORKSPACE_BYTES = 128 * 1024 * 1024
 
 
 def init_flashinfer_state(*, kv_pool: torch.Tensor, page_size: int, device,
-                          kv_scales: torch.Tensor | None = None) -> None:
+                          kv_scales: torch.Tensor | None = None,
+                          kv_scale_policy: str = "running") -> None:
     """Store the pool, allocate the 128 MiB workspace and the two wrappers
     (src/models/llama.py:39-67)."""
     if page_size != ops.PAGE_SIZE:
         raise NotImplementedError(f"page_size {page_size} (only 16 is implemented)")
+    if kv_scale_policy not in ("running", "fixed"):
+        raise ValueError(f"kv_scale_policy {kv_scale_policy!r}: 'running' or 'fixed'")
     FlashInferState.kv_pool = kv_pool
     FlashInferState.kv_scales = kv_scales
+    FlashInferState.kv_scale_policy = kv_scale_policy
     FlashInferState.page_size = page_size
     FlashInferState.dtype = kv_pool.dtype
     ws = torch.zeros(WORKSPACE_BYTES, dtype=torch.uint8, device=device)
@@ -148,16 +157,28 @@ def patched_llama_attention_forward(self, hidden_states: torch.Tensor,
     layer_scales = scales[self.layer_idx] if scales is not None else None
     ws = cast(torch.Tensor, FlashInferState.workspace_buffer)
     decode = FlashInferState.mode != "prefill"
+    running = (layer_scales is not None and pool.dtype == torch.float8_e4m3fn
+               and FlashInferState.kv_scale_policy == "running")
 
-    if FUSE and decode and _decode_rows_match(q_rows):
+    if running:
+        # e4m3 pages whose scales follow the rows written: RoPE, then the
+        # running-amax append (its scale updates are not fused into attention)
+        ops.apply_rope_pos_ids_inplace(q_rows, k_rows, positions, rope_theta=self.rope_theta,
+                                       rope_scale=self.rope_scale, interleave=False)
+        ops.append_paged_kv_cache_e4m3_amax(
+            k_rows, v_rows, cast(torch.Tensor, FlashInferState.batch_indices), positions,
+            layer_pool, cast(torch.Tensor, FlashInferState.kv_indices),
+            cast(torch.Tensor, FlashInferState.kv_indptr),
+            cast(torch.Tensor, FlashInferState.kv_last_page_len), layer_scales,
+            kv_layout="HND", error_flag=ws[:4].view(torch.int32))
+    elif FUSE and decode and _decode_rows_match(q_rows):
         # RoPE + append + attention of the decode step in one launch
         dw = cast(ops.BatchDecodeWithPagedKVCacheWrapper, FlashInferState.decode_wrapper)
         out = dw.run(q_rows, layer_pool, kv_scales=layer_scales, append_key=k_rows,
                      append_value=v_rows, rope=(self.rope_scale, self.rope_theta),
                      positions=positions)
         return self.o_proj(out.reshape(bsz, 1, self.num_heads * self.head_dim)), None
-
-    if FUSE:
+    elif FUSE:
         # RoPE + append in one launch, then attention
         ops.rope_append_paged_kv_cache(
             q_rows, k_rows, v_rows, cast(torch.Tensor, FlashInferState.batch_indices),

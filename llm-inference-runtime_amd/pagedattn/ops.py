@@ -17,8 +17,10 @@ Only the "HND" pool layout the engine uses is implemented
 engine never passes (positional encoding inside attention, sliding windows,
 logit soft-capping, custom masks) raise NotImplementedError.
 
-Additions with no FlashInfer counterpart: ``quantize_pages_e4m3`` and the
-``kv_scales`` argument for e4m3 pools with per-(page, K|V, kv-head) scales.
+Additions with no FlashInfer counterpart: ``quantize_pages_e4m3``, the
+``kv_scales`` argument for e4m3 pools with per-(page, K|V, kv-head) scales,
+``append_paged_kv_cache_e4m3_amax`` (e4m3 append that maintains those
+scales as pages fill) and ``fork_pages`` (copy-on-write page fork).
 """
 
 from __future__ import annotations
@@ -230,6 +232,121 @@ def rope_append_paged_kv_cache(q: torch.Tensor, append_key: torch.Tensor,
          ptr(pos), nnz, float(rope_scale), float(rope_theta), ptr(paged_kv_cache),
          dtype_code(paged_kv_cache.dtype), ptr(scales), num_pages, ptr(ind), ind.numel(),
          ptr(indptr), bsz, hkv, d, PAGE_SIZE, ptr(error_flag), _stream(device))
+
+
+def append_paged_kv_cache_e4m3_amax(append_key: torch.Tensor, append_value: torch.Tensor,
+                                    batch_indices: torch.Tensor, positions: torch.Tensor,
+                                    paged_kv_cache: torch.Tensor, kv_indices: torch.Tensor,
+                                    kv_indptr: torch.Tensor, kv_last_page_len: torch.Tensor,
+                                    kv_scales: torch.Tensor, kv_layout: str = "HND",
+                                    error_flag: torch.Tensor | None = None) -> None:
+    """append_paged_kv_cache into an e4m3 pool that keeps every (page, K|V,
+    kv-head) scale a running amax as the page fills (no FlashInfer
+    counterpart: the engine's fp8 write path).
+
+    Tokens of one sequence that land in one page must be consecutive and in
+    position order (what get_batch_indices_positions produces); the scale of
+    that page becomes max(old scale, smallest power of two s with 448 s >=
+    amax of the new rows) -- the old scale only counts when the page already
+    holds rows.  When the scale grows, the rows already in the page are
+    re-encoded with it (an exact exponent shift for values that stay in
+    e4m3's normal range).  kv_scales [num_pages, 2, Hkv] is updated in place.
+    Two sequences writing one page in the same call race: fork shared pages
+    first (fork_pages)."""
+    num_pages, hkv, d = _check_pool(paged_kv_cache, None, None, kv_layout)
+    if paged_kv_cache.dtype != torch.float8_e4m3fn:
+        raise ValueError("append_paged_kv_cache_e4m3_amax needs an e4m3 pool")
+    _check_rows(append_key, "append_key", hkv, d)
+    _check_rows(append_value, "append_value", hkv, d)
+    if append_key.dtype != append_value.dtype:
+        raise ValueError("append_key and append_value must share a dtype")
+    nnz = append_key.shape[0]
+    if append_value.shape[0] != nnz or batch_indices.numel() != nnz or positions.numel() != nnz:
+        raise ValueError("append_key/value, batch_indices and positions disagree on nnz")
+    scales = _check_scales(kv_scales, paged_kv_cache)
+    if scales is None or scales.data_ptr() != kv_scales.data_ptr():
+        raise ValueError("kv_scales must be contiguous: it is updated in place")
+    device = paged_kv_cache.device
+    bi = _i32(batch_indices, device)
+    pos = _i32(positions, device)
+    ind = _i32(kv_indices, device)
+    indptr = _i32(kv_indptr, device)
+    bsz = indptr.numel() - 1
+    if error_flag is not None and (error_flag.dtype != torch.int32 or error_flag.numel() < 1):
+        raise ValueError("error_flag must be an int32 device tensor")
+    call("pagedattn_append_paged_kv_cache_e4m3_amax", ptr(append_key), ptr(append_value),
+         append_key.stride(0), append_key.stride(1), append_value.stride(0),
+         append_value.stride(1), dtype_code(append_key.dtype), ptr(bi), ptr(pos), nnz,
+         ptr(paged_kv_cache), ptr(scales), num_pages, ptr(ind), ind.numel(), ptr(indptr), bsz,
+         hkv, d, PAGE_SIZE, ptr(error_flag), _stream(device))
+
+
+def fork_pages(kv_pool: torch.Tensor, src_pages, dst_pages, valid_tokens=None,
+               kv_scales: torch.Tensor | None = None,
+               error_flag: torch.Tensor | None = None) -> None:
+    """Copy-on-write fork of pages across every layer of the engine's pool
+    [L, num_pages, 2, Hkv, 16, D] (allocator.py:25-36 layout): for fork f,
+    rows [0, valid_tokens[f]) (all 16 when valid_tokens is None) of every
+    (K|V, kv-head) block of page src_pages[f] are copied to page
+    dst_pages[f] in every layer; e4m3 pools copy kv_scales [L, P, 2, Hkv]
+    entries too.  No FlashInfer counterpart: the reference's todo.md:17-19
+    asks for this before a sequence appends to a shared partial block.
+
+    Page lists given on the host are checked here (in range, destinations
+    distinct and not among the sources); device tensors are checked in the
+    kernel, which skips a bad fork and counts it in `error_flag`."""
+    _require_cuda(kv_pool, "kv_pool")
+    if kv_pool.dim() != 6 or kv_pool.shape[2] != 2 or kv_pool.shape[4] != PAGE_SIZE:
+        raise ValueError("kv_pool must be [L, num_pages, 2, num_kv_heads, 16, head_dim], "
+                         f"got {tuple(kv_pool.shape)}")
+    if not kv_pool.is_contiguous():
+        raise ValueError("kv_pool must be contiguous")
+    n_layers, num_pages, _, hkv, _, d = kv_pool.shape
+    device = kv_pool.device
+    scales = None
+    if kv_pool.dtype == torch.float8_e4m3fn:
+        if kv_scales is None:
+            raise ValueError("an e4m3 pool needs kv_scales [L, num_pages, 2, num_kv_heads]")
+        if (kv_scales.dtype != torch.float32 or not kv_scales.is_contiguous()
+                or tuple(kv_scales.shape) != (n_layers, num_pages, 2, hkv)):
+            raise ValueError(f"kv_scales must be contiguous float32 [{n_layers}, {num_pages}, "
+                             f"2, {hkv}], got {kv_scales.dtype} {tuple(kv_scales.shape)}")
+        _require_cuda(kv_scales, "kv_scales")
+        scales = kv_scales
+
+    def as_dev(x, name):
+        if isinstance(x, torch.Tensor) and x.device.type == "cuda":
+            return _i32(x, device), None
+        host = torch.as_tensor(x, dtype=torch.int64).reshape(-1)
+        return host.to(device=device, dtype=torch.int32), host
+
+    src, src_h = as_dev(src_pages, "src_pages")
+    dst, dst_h = as_dev(dst_pages, "dst_pages")
+    if src.numel() != dst.numel():
+        raise ValueError("src_pages and dst_pages differ in length")
+    valid = None
+    valid_h = None
+    if valid_tokens is not None:
+        valid, valid_h = as_dev(valid_tokens, "valid_tokens")
+        if valid.numel() != src.numel():
+            raise ValueError("valid_tokens must have one entry per fork")
+    if src_h is not None and dst_h is not None:
+        for name, h in (("src_pages", src_h), ("dst_pages", dst_h)):
+            if h.numel() and (int(h.min()) < 0 or int(h.max()) >= num_pages):
+                raise ValueError(f"{name} outside [0, {num_pages})")
+        moved = dst_h[dst_h != src_h]
+        if moved.unique().numel() != moved.numel():
+            raise ValueError("dst_pages must be distinct")
+        if bool(torch.isin(moved, src_h).any()):
+            raise ValueError("a destination page is also a source page")
+    if valid_h is not None and valid_h.numel() and (
+            int(valid_h.min()) < 0 or int(valid_h.max()) > PAGE_SIZE):
+        raise ValueError(f"valid_tokens outside [0, {PAGE_SIZE}]")
+    if error_flag is not None and (error_flag.dtype != torch.int32 or error_flag.numel() < 1):
+        raise ValueError("error_flag must be an int32 device tensor")
+    call("pagedattn_fork_pages", ptr(kv_pool), dtype_code(kv_pool.dtype), n_layers, num_pages,
+         hkv, d, PAGE_SIZE, ptr(scales), ptr(src), ptr(dst), ptr(valid), src.numel(),
+         ptr(error_flag), _stream(device))
 
 
 def quantize_pages_e4m3(pool: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -19,7 +19,8 @@ E4M3_MAX = 448.0
 
 __all__ = [
     "PAGE", "E4M3_MAX", "kv_lengths", "batch_indices_positions", "append_pages",
-    "e4m3_encode", "e4m3_decode", "quantize_pages", "append_pages_e4m3", "gather_pages",
+    "e4m3_encode", "e4m3_decode", "quantize_pages", "append_pages_e4m3", "pow2_scale",
+    "append_pages_e4m3_running", "fork_pages", "gather_pages",
     "attention", "decode", "prefill", "split_attention", "merge_states", "rope",
     "to_bits", "from_bits",
 ]
@@ -164,6 +165,105 @@ def append_pages_e4m3(pool_bits: np.ndarray, scales: torch.Tensor, k: torch.Tens
         out[page_id[js], 0, :, slot[js], :] = e4m3_encode(k[js].float(), ks)
         out[page_id[js], 1, :, slot[js], :] = e4m3_encode(v[js].float(), vs)
     return out, int((~ok).sum())
+
+
+def pow2_scale(amax) -> np.ndarray:
+    """Smallest power of two s with 448 * s >= amax, per element; 0 where
+    amax == 0; never below 2**-126.  With amax = m * 2**e (m in [0.5, 1)),
+    448 = 0.875 * 2**9 gives s = 2**(e - 9 + [m > 0.875]).
+    Pinned by: test_pow2_scale_brute (ldexp search over every exponent) and
+    test_running_amax_scale_bounds."""
+    a = np.asarray(amax, dtype=np.float32)
+    m, e = np.frexp(a)
+    ex = np.maximum(e.astype(np.int64) - 9 + (m > np.float32(0.875)), -126)
+    s = np.ldexp(np.float32(1.0), ex).astype(np.float32)
+    return np.where(a > 0, s, np.float32(0.0)).astype(np.float32)
+
+
+def _runs(bi: np.ndarray, pos: np.ndarray):
+    """Maximal runs of tokens that continue one another inside one page: token
+    t continues t - 1 iff same batch index, position + 1 and not a page start."""
+    n = len(bi)
+    t = 0
+    while t < n:
+        e = t + 1
+        while e < n and bi[e] == bi[e - 1] and pos[e] == pos[e - 1] + 1 and pos[e] % PAGE != 0:
+            e += 1
+        yield t, e
+        t = e
+
+
+def append_pages_e4m3_running(pool_bits: np.ndarray, scales: torch.Tensor, k: torch.Tensor,
+                              v: torch.Tensor, batch_indices, positions, kv_indices,
+                              kv_indptr):
+    """e4m3 page append that keeps each (page, K|V, head) scale a running
+    amax (no reference counterpart; the engine's fp8 write path).  Runs of
+    consecutive tokens landing in one page are applied in token order:
+      s_old = scale if the run starts past slot 0 else 0
+      s_new = max(s_old, pow2_scale(amax of the run's rows))
+      if s_new > s_old: rows [0, slot0) <- encode(decode(rows) * (s_old / s_new))
+      run rows <- encode(x / s_new)   (all zero codes when s_new == 0)
+    With power-of-two scales the re-encode is exact for values that stay in
+    e4m3's normal range.  Returns (new_pool_bits, new_scales, skipped).
+    Pinned by: test_running_append_one_shot_equals_incremental,
+    test_running_append_fresh_page_equals_direct and
+    test_running_amax_scale_bounds."""
+    out = pool_bits.copy()
+    sc = scales.clone().float()
+    bi = np.asarray(batch_indices, dtype=np.int64)
+    pos = np.asarray(positions, dtype=np.int64)
+    ok, page_id, slot = _append_targets(bi, pos, kv_indices, kv_indptr, pool_bits.shape[0])
+    skipped = 0
+    for t0, t1 in _runs(bi, pos):
+        if not ok[t0]:
+            skipped += t1 - t0
+            continue
+        pg = int(page_id[t0])
+        s0 = int(slot[t0])
+        for kind, src in ((0, k), (1, v)):
+            rows = src[t0:t1].float()  # [n, H, D]
+            amax = rows.abs().amax(dim=(0, 2)).numpy()  # [H]
+            s_old = sc[pg, kind].numpy() if s0 > 0 else np.zeros_like(amax)
+            s_new = np.maximum(s_old, pow2_scale(amax)).astype(np.float32)
+            for h in range(rows.shape[1]):
+                if s0 > 0 and s_new[h] > s_old[h]:
+                    r = np.float32(s_old[h]) / np.float32(s_new[h])
+                    old = e4m3_decode(out[pg, kind, h, :s0], 1.0) * torch.tensor(r)
+                    out[pg, kind, h, :s0] = (
+                        old.clamp(-E4M3_MAX, E4M3_MAX).to(torch.float8_e4m3fn)
+                        .view(torch.uint8).numpy())
+                if s_new[h] > 0:
+                    out[pg, kind, h, s0:s0 + (t1 - t0)] = e4m3_encode(rows[:, h], s_new[h])
+                else:
+                    out[pg, kind, h, s0:s0 + (t1 - t0)] = 0
+                sc[pg, kind, h] = float(s_new[h])
+    return out, sc, skipped
+
+
+def fork_pages(pool_bits: np.ndarray, src_pages, dst_pages, valid_tokens=None,
+               scales: torch.Tensor | None = None):
+    """Copy-on-write page fork over a whole pool [L, P, 2, H, 16, D]
+    (allocator.py:25-36 layout; the fork itself is the CoW step the
+    reference's todo.md:17-19 asks for): for every fork f and layer l,
+    rows [0, n_f) of every (K|V, head) block of page src_f are copied to
+    page dst_f (n_f = valid_tokens[f], 16 when absent); scales [L, P, 2, H]
+    follow.  Forks with a page or count out of range are skipped and counted.
+    Returns (new_pool_bits, new_scales, skipped).
+    Pinned by: test_fork_pages_loop (pure-Python loop) and
+    test_fork_then_gather."""
+    out = pool_bits.copy()
+    sc = scales.clone() if scales is not None else None
+    num_pages = pool_bits.shape[1]
+    skipped = 0
+    for f, (s, d) in enumerate(zip(src_pages, dst_pages)):
+        n = PAGE if valid_tokens is None else int(valid_tokens[f])
+        if not (0 <= s < num_pages and 0 <= d < num_pages and 0 <= n <= PAGE):
+            skipped += 1
+            continue
+        out[:, d, :, :, :n, :] = pool_bits[:, s, :, :, :n, :]
+        if sc is not None:
+            sc[:, d] = scales[:, s]
+    return out, sc, skipped
 
 
 # -----------------------------------------------------------------------------

@@ -12,6 +12,7 @@ import pytest
 import torch
 
 from pagedattn import llama as L
+from pagedattn.capacity import new_kv_scales
 from pagedattn.metadata import decode_metadata, prefill_metadata
 
 from paged_cases import i32, random_tables
@@ -29,13 +30,18 @@ def _tiny_llama():
     return LlamaForCausalLM(cfg).eval()
 
 
-def _run_paged(model, device, tokens, lens, tables, num_pages, fuse):
+def _run_paged(model, device, tokens, lens, tables, num_pages, fuse, kv_dtype=torch.bfloat16):
     cfg = model.config
     hkv, d = cfg.num_key_value_heads, cfg.hidden_size // cfg.num_attention_heads
-    pool = torch.zeros((cfg.num_hidden_layers, num_pages, 2, hkv, 16, d), dtype=torch.bfloat16,
-                       device=device)
+    shape = (cfg.num_hidden_layers, num_pages, 2, hkv, 16, d)
+    if kv_dtype == torch.float8_e4m3fn:
+        pool = torch.zeros(shape, dtype=torch.uint8, device=device).view(kv_dtype)
+    else:
+        pool = torch.zeros(shape, dtype=kv_dtype, device=device)
     L.FUSE = fuse
-    L.init_flashinfer_state(kv_pool=pool, page_size=16, device=device)
+    scales = new_kv_scales(pool) if kv_dtype == torch.float8_e4m3fn else None
+    L.init_flashinfer_state(kv_pool=pool, page_size=16, device=device, kv_scales=scales,
+                            kv_scale_policy="running")
     # prefill: every sequence's first lens[b] tokens in one packed forward
     meta = prefill_metadata(tables, [0] * len(lens), lens)
     L.build_batch_indices_positions(i32(meta.qo_indptr, device), i32(meta.seq_lens, device))
@@ -59,7 +65,7 @@ def _run_paged(model, device, tokens, lens, tables, num_pages, fuse):
     step = torch.stack([tokens[b, n] for b, n in enumerate(lens)])[:, None]
     with torch.no_grad():
         dec = model(input_ids=step, use_cache=False).logits[:, 0]
-    return pre_last.float(), dec.float()
+    return pre_last.float(), dec.float(), scales
 
 
 def test_patched_llama_matches_eager_model(gpu):
@@ -78,10 +84,33 @@ def test_patched_llama_matches_eager_model(gpu):
     assert torch.equal(fused[0], plain[0])
     assert torch.equal(fused[1], plain[1])
     # and both follow the model's own attention over the whole sequence
+    _check_against_model(ref, tokens, lens, fused, 3e-2)
+
+
+def _check_against_model(ref, tokens, lens, got_logits, tol):
     with torch.no_grad():
         for b, n in enumerate(lens):
             full = ref(input_ids=tokens[b:b + 1, :n + 1], use_cache=False).logits[0].float()
-            for got, want in ((fused[0][b], full[n - 1]), (fused[1][b], full[n])):
+            for got, want in ((got_logits[0][b], full[n - 1]), (got_logits[1][b], full[n])):
                 got = got.cpu()
                 rel = float((got - want).norm() / want.norm())
-                assert rel < 3e-2, (b, rel)
+                assert rel < tol, (b, rel)
+
+
+def test_patched_llama_e4m3_pool_running_scales(gpu):
+    """An e4m3 pool written by the engine itself: every append keeps its
+    pages' scales a running amax (powers of two)."""
+    ref = _tiny_llama()
+    model = copy.deepcopy(ref).to(device=gpu, dtype=torch.bfloat16)
+    L.patch_llama_model(model)
+    lens = [37, 100, 5, 64]
+    rng = np.random.default_rng(1)
+    tokens = torch.as_tensor(rng.integers(0, ref.config.vocab_size, size=(len(lens), 128)))
+    tables, num_pages = random_tables(rng, [n + 1 for n in lens], extra_pages=4)
+    out = _run_paged(model, gpu, tokens.to(gpu), lens, tables, num_pages, fuse=True,
+                     kv_dtype=torch.float8_e4m3fn)
+    used = sorted({p for t in tables for p in t})
+    sc = out[2][:, used].cpu()
+    assert bool((sc > 0).all())
+    assert bool((torch.frexp(sc).mantissa == 0.5).all())
+    _check_against_model(ref, tokens, lens, out, 8e-2)

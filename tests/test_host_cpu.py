@@ -170,3 +170,66 @@ def test_work_formulas_brute_force():
     want = (int(d.meta.seq_lens.sum()) * 4 * 64 * 2 * 2 + 8 * 32 * 64 * 4
             + 4 * (len(d.meta.kv_indices) + 17))
     assert W.decode_bytes(d, 2) == want
+
+
+def test_bytes_per_block_and_sizing():
+    from pagedattn import capacity as C
+    # the reference's rule (capacity.py:16-32): layers x 2 x heads x block x dim x element size
+    assert C.bytes_per_block(16, 32, 8, 128, torch.bfloat16) == 32 * 2 * 8 * 16 * 128 * 2
+    assert C.bytes_per_block(16, 22, 4, 64, torch.float16) == 22 * 2 * 4 * 16 * 64 * 2
+    # e4m3: one byte per element plus an fp32 scale per (layer, K|V, head)
+    assert C.bytes_per_block(16, 80, 8, 128, torch.float8_e4m3fn) == \
+        80 * 2 * 8 * 16 * 128 + 80 * 2 * 8 * 4
+    per = C.bytes_per_block(16, 32, 8, 128, torch.bfloat16)
+    free = 100 * 1024 ** 3
+    usable = free - max(2 * 1024 ** 3, int(free * 0.15))
+    assert C.blocks_for_free_bytes(free, 16, 32, 8, 128, torch.bfloat16) == usable // per
+    with pytest.raises(RuntimeError, match="need at least"):
+        C.blocks_for_free_bytes(3 * 1024 ** 3, 16, 32, 8, 128, torch.bfloat16, min_blocks=10 ** 6)
+    assert C.estimate_num_blocks(torch.device("cpu"), 16, 32, 8, 128, torch.bfloat16) == -1
+
+
+class _FakeAllocator:
+    def __init__(self, n):
+        self.free_blocks = list(range(n))
+        self.ref_counts = [0] * n
+
+    def allocate(self, n):
+        if len(self.free_blocks) < n:
+            raise RuntimeError("Not enough free KV blocks")
+        out, self.free_blocks = self.free_blocks[:n], self.free_blocks[n:]
+        for b in out:
+            self.ref_counts[b] = 1
+        return out
+
+    def decref(self, blocks):
+        for b in blocks:
+            self.ref_counts[b] -= 1
+            if self.ref_counts[b] == 0:
+                self.free_blocks.append(b)
+
+
+def test_cow_fork_decisions(monkeypatch):
+    from pagedattn import cow
+    calls = []
+    monkeypatch.setattr(cow.ops, "fork_pages",
+                        lambda pool, src, dst, valid_tokens=None, kv_scales=None:
+                        calls.append((list(src), list(dst), list(valid_tokens))))
+    a = _FakeAllocator(10)
+    t_shared = a.allocate(2)            # [0, 1]
+    for b in t_shared:
+        a.ref_counts[b] = 2             # shared by sequences 0 and 1
+    tables = [list(t_shared), list(t_shared), a.allocate(1), list(t_shared[:1])]
+    a.ref_counts[0] += 1                # sequence 3 shares page 0 too
+    # seq 0: next token in shared partial page 1 -> fork; seq 1: page 1 now
+    # held by seq 1 alone -> no fork; seq 2: own page; seq 3: page 0 full -> no fork
+    forks = cow.fork_for_append(a, tables, [20, 20, 3, 16], None)
+    assert forks == [(0, 1, 3)]
+    assert calls == [([1], [3], [4])]
+    assert tables[0] == [0, 3] and tables[1] == [0, 1]
+    assert a.ref_counts[1] == 1 and a.ref_counts[3] == 1
+    with pytest.raises(RuntimeError, match="Not enough"):
+        a2 = _FakeAllocator(1)
+        p = a2.allocate(1)
+        a2.ref_counts[p[0]] = 2
+        cow.fork_for_append(a2, [p], [5], None)
