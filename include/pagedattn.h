@@ -192,6 +192,34 @@ int pagedattn_fork_pages(void* kv_pool, int32_t pool_dtype, int32_t num_layers,
                          const int32_t* dst_pages, const int32_t* valid_tokens,
                          int32_t num_forks, int32_t* error_flag, void* stream);
 
+/* Step metadata built on the device (replaces the Python list building and
+ * upload of src/engine/runtime/step_executor.py:98-165 (prefill) and
+ * :204-234 (decode), and the device-to-host sync of
+ * build_batch_indices_positions, src/models/llama.py:70-83).
+ * block_tables: [batch_size, table_stride] int32, the first max_pages
+ * entries of row b are sequence b's pages; kv_lens[b]: tokens in the cache
+ * once this step's tokens are appended; new_lens[b]: tokens this step adds
+ * (NULL: a decode step, one token per sequence, token row b = sequence b).
+ * Outputs (device, int32):
+ *   kv_indptr [batch_size + 1], kv_indices [indices_capacity]: the first
+ *     ceil(kv_lens[b] / 16) entries of every row (the decode step too; the
+ *     reference passes the whole row, step_executor.py:209),
+ *   kv_last_page_len [batch_size] = kv_lens % 16 or 16,
+ *   qo_indptr [batch_size + 1] (may be NULL for decode): prefix sum of the
+ *     new token counts,
+ *   batch_indices / positions [tokens_capacity]: sequence and position of
+ *     every new token (kv_lens[b] - n .. kv_lens[b] - 1).
+ * Two launches with fixed shapes (graph-capturable).  A row needing more
+ * than max_pages pages, or outputs beyond a capacity, are dropped and
+ * counted in *error_flag. */
+int pagedattn_build_paged_metadata(const int32_t* block_tables, int64_t table_stride,
+                                   int32_t max_pages, const int32_t* kv_lens,
+                                   const int32_t* new_lens, int32_t batch_size,
+                                   int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
+                                   int32_t indices_capacity, int32_t* kv_last_page_len,
+                                   int32_t* batch_indices, int32_t* positions,
+                                   int32_t tokens_capacity, int32_t* error_flag, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Plans.  pagedattn_plan_create/destroy manage the host object.
  * BatchDecodeWithPagedKVCacheWrapper.begin_forward(kv_indptr, kv_indices,
@@ -212,6 +240,24 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
                           int32_t page_size, int32_t split_pages,
                           void* workspace, size_t workspace_bytes,
                           void* stream);
+
+/* Decode plan that reads no metadata on the host: the
+ * BatchDecodeWithPagedKVCacheWrapper(use_cuda_graph=True) counterpart of
+ * begin_forward (src/models/llama.py:133-147; the reference's todo.md:14
+ * asks for CUDA-graph decode).  Only the batch size and head shape are
+ * fixed here; every pagedattn_decode_run* with this plan partitions the
+ * work on the device from the kv_indptr it is given (the balanced split of
+ * pagedattn_decode_plan with split_pages = 0: the (sequence, head group,
+ * page) stream cut into equal shares, one share per head group of waves),
+ * then merges cut sequences in a second launch over all (sequence, kv head)
+ * pairs.  Both launches have fixed shapes, no host synchronisation and no
+ * memsets, so a run can be captured in a HIP graph and replayed while the
+ * metadata and pool change in place.  The workspace holds the split
+ * partials only (2 x shares x head-group waves slots). */
+int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
+                                 int32_t num_qo_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, int32_t page_size, void* workspace,
+                                 size_t workspace_bytes);
 
 /* BatchDecodeWithPagedKVCacheWrapper.forward(q, paged_kv_cache)
  * (src/models/llama.py:230-245).  q [batch, num_qo_heads, head_dim] strided;

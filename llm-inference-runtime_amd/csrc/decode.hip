@@ -193,6 +193,48 @@ struct Stage {
 
 // Page ids of a pair, fetched with scalar loads two pairs ahead of use
 // (-1: absent or invalid page).
+// Device-side decode partition (plans made with pagedattn_decode_plan_device):
+// stream = (pages of all sequences) x (head groups per sequence), cut into
+// shares of `share` pages, share >= 4 and even, with at most n_groups shares.
+// The same rule as the host planner's balanced split.
+struct ImplicitSplit {
+  int64_t stream, share;
+  int base, ngrp;
+};
+
+__device__ __forceinline__ ImplicitSplit implicit_split(const int32_t* kv_indptr, int batch,
+                                                        int ngrp, int n_groups) {
+  ImplicitSplit sp;
+  sp.ngrp = ngrp;
+  sp.base = uniform(load_invariant(kv_indptr));
+  const int top = uniform(load_invariant(kv_indptr + batch));
+  sp.stream = (int64_t)ngrp * max(0, top - sp.base);
+  int64_t t = (sp.stream + n_groups - 1) / n_groups;
+  t = (t + 1) / 2 * 2;
+  sp.share = max<int64_t>(4, t);
+  return sp;
+}
+
+// Largest b in [0, batch) with ngrp * (kv_indptr[b] - base) <= x, by a
+// 64-way search: each round every lane tests one candidate of the range and
+// the ballot narrows it 64-fold.  Always ends (the range shrinks every
+// round) and stays in [0, batch) whatever kv_indptr holds.
+__device__ __forceinline__ int find_sequence(const int32_t* kv_indptr, int batch, int ngrp,
+                                             int base, int64_t x, int lane) {
+  int lo = 0, hi = batch;
+  while (hi - lo > 1) {
+    const int step = (hi - lo + kWave - 1) / kWave;
+    const int c = lo + lane * step;
+    bool ok = false;
+    if (c < hi) ok = (int64_t)ngrp * (kv_indptr[c] - base) <= x;
+    const int cnt = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
+    const int nlo = lo + max(cnt - 1, 0) * step;
+    hi = uniform(min(nlo + step, hi));
+    lo = uniform(nlo);
+  }
+  return lo;
+}
+
 struct PairIds {
   int p0, p1;
 };
@@ -442,7 +484,7 @@ __device__ __forceinline__ void fused_append(const DecodeParams& p,
                           *reinterpret_cast<const u32x4*>(src + 8 * c));
 }
 
-template <int D, bool BF16, bool FP8, bool APPEND, bool ROPE>
+template <int D, bool BF16, bool FP8, bool APPEND, bool ROPE, bool IMPLICIT>
 __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
@@ -463,22 +505,13 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
   const int G = lane >> 4;
   const int g = p.g;
 
-  const int it_lo = uniform(load_invariant(p.wave_ptr + gw));
-  const int it_hi = uniform(load_invariant(p.wave_ptr + gw + 1));
-  for (int it = it_lo; it < it_hi; ++it) {
-    const int32_t* itp = reinterpret_cast<const int32_t*>(p.items + it);
-    const int b = uniform(load_invariant(itp + 0));
-    const int h0 = uniform(load_invariant(itp + 1));
-    const int item_lo = uniform(load_invariant(itp + 2));
-    const int item_hi = uniform(load_invariant(itp + 3));
-    const int slot0 = uniform(load_invariant(itp + 4));
-    const int merge = uniform(load_invariant(itp + 5));
+  // one work item: pages [item_lo, item_hi) of sequence b for KV heads
+  // h0 + [0, hg); slot0 >= 0: the item is one piece of a cut sequence and
+  // writes split partials to slots slot0 + wi
+  auto run_item = [&](const int b, const int h0, const int item_lo, const int item_hi,
+                      const int slot0) {
     const int h = h0 + wi;
     const int slot = slot0 >= 0 ? slot0 + wi : -1;
-    // a work list that does not match this launch is skipped, never followed
-    if (b < 0 || b >= p.batch_size || h0 < 0 || h >= p.hkv ||
-        slot >= p.n_slots || merge >= p.n_merge || (slot >= 0) != (merge >= 0))
-      continue;
     const int ind_lo = uniform(load_invariant(p.kv_indptr + b));
     const int npages = max(0, uniform(load_invariant(p.kv_indptr + b + 1)) - ind_lo);
     const int last = min(max(uniform(load_invariant(p.last_page_len + b)), 1), kPage);
@@ -623,6 +656,64 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
         if (G == 0) p.partial_lse[(int64_t)slot * g + n] = lse2;
       }
     }
+  };
+
+  if constexpr (!IMPLICIT) {
+    const int it_lo = uniform(load_invariant(p.wave_ptr + gw));
+    const int it_hi = uniform(load_invariant(p.wave_ptr + gw + 1));
+    for (int it = it_lo; it < it_hi; ++it) {
+      const int32_t* itp = reinterpret_cast<const int32_t*>(p.items + it);
+      const int b = uniform(load_invariant(itp + 0));
+      const int h0 = uniform(load_invariant(itp + 1));
+      const int item_lo = uniform(load_invariant(itp + 2));
+      const int item_hi = uniform(load_invariant(itp + 3));
+      const int slot0 = uniform(load_invariant(itp + 4));
+      const int merge = uniform(load_invariant(itp + 5));
+      const int slot = slot0 >= 0 ? slot0 + wi : -1;
+      // a work list that does not match this launch is skipped, never followed
+      if (b < 0 || b >= p.batch_size || h0 < 0 || h0 + wi >= p.hkv ||
+          slot >= p.n_slots || merge >= p.n_merge || (slot >= 0) != (merge >= 0))
+        continue;
+      run_item(b, h0, item_lo, item_hi, slot0);
+    }
+  } else {
+    // Device-side partition, read from kv_indptr at run time: the stream of
+    // (sequence, head group, page) triples in sequence-major order is cut
+    // into equal shares of T pages, share gw for head group gw.  A sequence
+    // cut by a share boundary leaves at most two pieces in one share (its
+    // first and its last item); they write slots 2 gw and 2 gw + 1.
+    const ImplicitSplit sp = implicit_split(p.kv_indptr, p.batch_size, p.hkv >> p.hg_shift,
+                                            p.n_groups);
+    const int64_t start = (int64_t)gw * sp.share;
+    if (start >= sp.stream) return;
+    const int64_t end = min(start + sp.share, sp.stream);
+    const int ngrp = sp.ngrp;
+    int b = find_sequence(p.kv_indptr, p.batch_size, ngrp, sp.base, start, lane);
+    int ind_lo = uniform(load_invariant(p.kv_indptr + b));
+    int np = uniform(load_invariant(p.kv_indptr + b + 1)) - ind_lo;
+    int hgrp = np > 0 ? (int)min<int64_t>(ngrp, max<int64_t>(0, (start - (int64_t)ngrp *
+                                                                          (ind_lo - sp.base)) / np))
+                      : ngrp;
+    int64_t pos = start;
+    while (pos < end) {
+      if (hgrp >= ngrp) {
+        if (++b >= p.batch_size) break;
+        ind_lo = uniform(load_invariant(p.kv_indptr + b));
+        np = uniform(load_invariant(p.kv_indptr + b + 1)) - ind_lo;
+        hgrp = np > 0 ? 0 : ngrp;
+        continue;
+      }
+      const int64_t s_off = (int64_t)ngrp * (ind_lo - sp.base) + (int64_t)hgrp * np;
+      const int64_t lo = max<int64_t>(0, pos - s_off);
+      const int64_t hi = min<int64_t>(np, end - s_off);
+      if (hi > lo) {
+        const bool cut = lo > 0 || hi < np;
+        const int slot0 = cut ? (2 * gw + (pos == start ? 0 : 1)) << p.hg_shift : -1;
+        run_item(b, hgrp << p.hg_shift, (int)lo, (int)hi, slot0);
+        pos = s_off + hi;
+      }
+      ++hgrp;
+    }
   }
 }
 
@@ -661,25 +752,90 @@ __global__ void __launch_bounds__(128)
         M != -INFINITY ? (M + log2f(den)) * 0.69314718055994531f : -INFINITY;
 }
 
+// Split-KV merge of a device-side partition, one workgroup per (sequence,
+// KV head, query head of its group), one thread per d: the pieces of a cut (sequence, head group) segment sit in shares
+// first..last; the piece in share w wrote slot (2 w + j) * hg + wi with j = 1
+// only for the first share when the segment starts inside it.  Empty
+// sequences get zero output and lse = -inf here (the attention launch has no
+// item for them); uncut segments were written by the attention launch.
+struct MergeImplicitArgs {
+  const int32_t* kv_indptr;
+  const float* po;
+  const float* pl;
+  uint16_t* out;
+  float* lse;
+  int32_t batch, hq, hkv, g, d, hg_shift, n_groups;
+};
+
+template <bool BF16>
+__global__ void __launch_bounds__(128) decode_merge_implicit_kernel(MergeImplicitArgs a) {
+  const int b = blockIdx.x / a.hkv;
+  const int h = blockIdx.x % a.hkv;
+  const int hn = blockIdx.y;  // query head within the group
+  const int dd = threadIdx.x;
+  const int head = h * a.g + hn;
+  const int ngrp = a.hkv >> a.hg_shift;
+  const ImplicitSplit sp = implicit_split(a.kv_indptr, a.batch, ngrp, a.n_groups);
+  const int ind_lo = load_invariant(a.kv_indptr + b);
+  const int np = load_invariant(a.kv_indptr + b + 1) - ind_lo;
+  uint16_t* orow = a.out + ((int64_t)b * a.hq + head) * a.d;
+  if (np <= 0) {
+    if (dd < a.d) orow[dd] = f2h<BF16>(0.f);
+    if (a.lse && dd == 0) a.lse[(int64_t)b * a.hq + head] = -INFINITY;
+    return;
+  }
+  const int64_t s_off = (int64_t)ngrp * (ind_lo - sp.base) + (int64_t)(h >> a.hg_shift) * np;
+  const int64_t first = s_off / sp.share;
+  const int64_t last = (s_off + np - 1) / sp.share;
+  if (s_off < 0 || first == last || last >= a.n_groups) return;
+  const int wi = h & ((1 << a.hg_shift) - 1);
+  auto slot_of = [&](int64_t w) {
+    const int j = (w == first && s_off != w * sp.share) ? 1 : 0;
+    return ((2 * w + j) << a.hg_shift) + wi;
+  };
+  float M = -INFINITY;
+  for (int64_t w = first; w <= last; ++w) M = fmaxf(M, a.pl[slot_of(w) * a.g + hn]);
+  float num = 0.f, den = 0.f;
+  if (M != -INFINITY) {
+    for (int64_t w = first; w <= last; ++w) {
+      const int64_t sh = slot_of(w) * a.g + hn;
+      const float wt = exp2f(a.pl[sh] - M);
+      den += wt;
+      if (dd < a.d) num += wt * a.po[sh * a.d + dd];
+    }
+  }
+  if (dd < a.d) orow[dd] = f2h<BF16>(M != -INFINITY ? num / den : 0.f);
+  if (a.lse && dd == 0)
+    a.lse[(int64_t)b * a.hq + head] =
+        M != -INFINITY ? (M + log2f(den)) * 0.69314718055994531f : -INFINITY;
+}
+
 // ----------------------------------------------------------------------------
 // launch table
 using DecodeFn = void (*)(DecodeParams);
 
-template <int D, bool BF16, bool FP8>
+template <int D, bool BF16, bool FP8, bool IMPLICIT>
 DecodeFn decode_fn(bool append, bool rope) {
-  if (!append) return decode_kernel<D, BF16, FP8, false, false>;
-  return rope ? decode_kernel<D, BF16, FP8, true, true> : decode_kernel<D, BF16, FP8, true, false>;
+  if (!append) return decode_kernel<D, BF16, FP8, false, false, IMPLICIT>;
+  return rope ? decode_kernel<D, BF16, FP8, true, true, IMPLICIT>
+              : decode_kernel<D, BF16, FP8, true, false, IMPLICIT>;
 }
 
-static DecodeFn pick_decode(int d, bool bf16, bool fp8, bool append, bool rope) {
-  if (d == 64) {
-    if (bf16)
-      return fp8 ? decode_fn<64, true, true>(append, rope) : decode_fn<64, true, false>(append, rope);
-    return fp8 ? decode_fn<64, false, true>(append, rope) : decode_fn<64, false, false>(append, rope);
-  }
+template <int D, bool IMPLICIT>
+DecodeFn decode_fn_d(bool bf16, bool fp8, bool append, bool rope) {
   if (bf16)
-    return fp8 ? decode_fn<128, true, true>(append, rope) : decode_fn<128, true, false>(append, rope);
-  return fp8 ? decode_fn<128, false, true>(append, rope) : decode_fn<128, false, false>(append, rope);
+    return fp8 ? decode_fn<D, true, true, IMPLICIT>(append, rope)
+               : decode_fn<D, true, false, IMPLICIT>(append, rope);
+  return fp8 ? decode_fn<D, false, true, IMPLICIT>(append, rope)
+             : decode_fn<D, false, false, IMPLICIT>(append, rope);
+}
+
+static DecodeFn pick_decode(int d, bool bf16, bool fp8, bool append, bool rope, bool implicit) {
+  if (d == 64)
+    return implicit ? decode_fn_d<64, true>(bf16, fp8, append, rope)
+                    : decode_fn_d<64, false>(bf16, fp8, append, rope);
+  return implicit ? decode_fn_d<128, true>(bf16, fp8, append, rope)
+                  : decode_fn_d<128, false>(bf16, fp8, append, rope);
 }
 
 // Waves the planner spreads the work over, per CU (one wave per SIMD keeps
@@ -882,6 +1038,7 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   if (rc) return rc;
 
   char* ws = static_cast<char*>(workspace);
+  plan->implicit = false;
   plan->batch_size = batch_size;
   plan->hq = num_qo_heads;
   plan->hkv = num_kv_heads;
@@ -899,6 +1056,58 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   plan->partial_lse = reinterpret_cast<float*>(ws + off_pl);
   plan->total_pages = total;
   plan->max_pages = maxp;
+  plan->mode = kPlanDecode;
+  return PAGEDATTN_OK;
+}
+
+int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
+                                 int32_t num_qo_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, int32_t page_size, void* workspace,
+                                 size_t workspace_bytes) {
+  const char* who = "decode_plan_device";
+  if (!plan) return set_error(PAGEDATTN_ERR_INVALID, "%s: null plan", who);
+  plan->mode = kPlanNone;
+  if (batch_size < 0)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: batch_size %d < 0", who, batch_size);
+  int rc = validate_heads(who, num_qo_heads, num_kv_heads, head_dim, page_size);
+  if (rc) return rc;
+  if (!workspace || ((uintptr_t)workspace & (kWsAlign - 1)))
+    return set_error(PAGEDATTN_ERR_INVALID,
+                     "%s: workspace must be a 256-byte aligned device buffer", who);
+  int cus = device_cu_count();
+  if (cus <= 0) cus = 256;
+  const int hg = decode_head_group(num_kv_heads);
+  const int g = num_qo_heads / num_kv_heads;
+  const int n_groups = std::max(1, cus * decode_waves_per_cu() / hg);
+  const int n_slots = 2 * n_groups * hg;
+  const size_t off_po = ws_align(kWsHeader);
+  const size_t off_pl = ws_align(off_po + sizeof(float) * (size_t)n_slots * g * head_dim);
+  const size_t end = ws_align(off_pl + sizeof(float) * (size_t)n_slots * g);
+  if (end > workspace_bytes)
+    return set_error(PAGEDATTN_ERR_WORKSPACE, "%s: needs %zu workspace bytes, %zu available",
+                     who, end, workspace_bytes);
+  char* ws = static_cast<char*>(workspace);
+  plan->host.clear();
+  plan->workspace = workspace;
+  plan->workspace_bytes = workspace_bytes;
+  plan->implicit = true;
+  plan->batch_size = batch_size;
+  plan->hq = num_qo_heads;
+  plan->hkv = num_kv_heads;
+  plan->d = head_dim;
+  plan->page_size = page_size;
+  plan->n_items = n_groups;
+  plan->hg_shift = hg == 4 ? 2 : hg == 2 ? 1 : 0;
+  plan->n_merge = 0;
+  plan->n_slots = n_slots;
+  plan->split_pages = 0;
+  plan->items_dev = nullptr;
+  plan->wave_ptr_dev = nullptr;
+  plan->merge_dev = nullptr;
+  plan->partial_o = reinterpret_cast<float*>(ws + off_po);
+  plan->partial_lse = reinterpret_cast<float*>(ws + off_pl);
+  plan->total_pages = -1;
+  plan->max_pages = -1;
   plan->mode = kPlanDecode;
   return PAGEDATTN_OK;
 }
@@ -992,11 +1201,24 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
 
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = q_dtype == PAGEDATTN_BF16;
-  DecodeFn fn = pick_decode(plan->d, bf16, fp8, app != nullptr, app && app->rope);
+  DecodeFn fn = pick_decode(plan->d, bf16, fp8, app != nullptr, app && app->rope,
+                            plan->implicit);
   const int blocks = ((plan->n_items << plan->hg_shift) + 3) / 4;
   hipLaunchKernelGGL(fn, dim3(blocks), dim3(256), 0, s, p);
   int rc = check_launch(who);
-  if (rc || plan->n_merge == 0) return rc;
+  if (rc) return rc;
+  if (plan->implicit) {
+    MergeImplicitArgs m{kv_indptr, plan->partial_o, plan->partial_lse, p.out, lse,
+                        plan->batch_size, plan->hq, plan->hkv, p.g, plan->d,
+                        plan->hg_shift, plan->n_items};
+    const dim3 grid((unsigned)((int64_t)plan->batch_size * plan->hkv), p.g);
+    if (bf16)
+      hipLaunchKernelGGL(decode_merge_implicit_kernel<true>, grid, dim3(plan->d), 0, s, m);
+    else
+      hipLaunchKernelGGL(decode_merge_implicit_kernel<false>, grid, dim3(plan->d), 0, s, m);
+    return check_launch("decode_run(merge)");
+  }
+  if (plan->n_merge == 0) return rc;
   const dim3 grid(plan->n_merge, p.g);
   const MergeItem* merges = static_cast<const MergeItem*>(plan->merge_dev);
   if (bf16)

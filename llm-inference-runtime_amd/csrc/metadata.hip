@@ -1,0 +1,191 @@
+// Device-side paged metadata: what the engine's step executor builds in
+// Python lists and uploads every step (src/engine/runtime/step_executor.py:
+// 98-165 for a chunked-prefill step, :204-234 for a decode step) and what
+// build_batch_indices_positions derives after a device-to-host sync
+// (src/models/llama.py:70-83), built on the GPU from a fixed-capacity block
+// table and the sequence lengths.  No host round trip, fixed launch shapes,
+// no memsets: the whole step can be captured in a HIP graph.
+//
+// Per sequence b with kv length L (tokens in the cache after this step's
+// appends, including them) and n new tokens:
+//   pages   = ceil(L / 16), the table cut to the pages in use (the reference
+//             decode step passes the whole table, step_executor.py:209, which
+//             overstates kv_len by a page whenever L % 16 == 0)
+//   last    = L % 16, or 16
+//   tokens  = positions L - n .. L - 1 (decode: one token, row b)
+#include <algorithm>
+
+#include "common.h"
+
+namespace pa {
+
+struct MetaArgs {
+  const int32_t* tables;
+  int64_t stride;
+  int32_t max_pages;
+  const int32_t* kv_lens;
+  const int32_t* new_lens;  // null: decode, one new token per sequence
+  int32_t batch;
+  int32_t* qo_indptr;
+  int32_t* kv_indptr;
+  int32_t* kv_indices;
+  int32_t indices_cap;
+  int32_t* last;
+  int32_t* bi;
+  int32_t* pos;
+  int32_t tokens_cap;
+  int32_t* err;
+};
+
+constexpr int kMetaThreads = 1024;
+
+__device__ __forceinline__ int seq_pages(const MetaArgs& a, int L) {
+  const int np = L > 0 ? (L + kPage - 1) / kPage : 0;
+  return min(np, a.max_pages);
+}
+
+__device__ __forceinline__ int seq_new_tokens(const MetaArgs& a, int b, int L) {
+  if (!a.new_lens) return 1;
+  return min(max(a.new_lens[b], 0), max(L, 0));
+}
+
+// Exclusive prefix sum over the 1024 threads of the workgroup; *total gets
+// the sum.  `red` holds 16 wave totals.
+__device__ __forceinline__ int block_excl_scan(int v, int* total, int* red) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == kWave - 1) red[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kMetaThreads / kWave; ++w) {
+    const int t = red[w];
+    before += w < wave ? t : 0;
+    all += t;
+  }
+  __syncthreads();
+  *total = all;
+  return before + x - v;
+}
+
+// One workgroup: page and token offsets of every sequence, last page
+// lengths, and (decode) the token -> sequence / position rows.
+__global__ void __launch_bounds__(kMetaThreads) meta_scan_kernel(MetaArgs a) {
+  __shared__ int red[2][kMetaThreads / kWave];
+  int run_pages = 0, run_tokens = 0;
+  bool clipped = false;
+  for (int base = 0; base < a.batch; base += kMetaThreads) {
+    const int b = base + (int)threadIdx.x;
+    const int L = b < a.batch ? a.kv_lens[b] : 0;
+    const int full = L > 0 ? (L + kPage - 1) / kPage : 0;
+    const int np = b < a.batch ? seq_pages(a, L) : 0;
+    const int nt = b < a.batch ? seq_new_tokens(a, b, L) : 0;
+    clipped |= full > np;
+    int tot_p, tot_t;
+    const int ep = block_excl_scan(np, &tot_p, red[0]);
+    const int et = block_excl_scan(nt, &tot_t, red[1]);
+    if (b < a.batch) {
+      a.kv_indptr[b] = run_pages + ep;
+      if (a.qo_indptr) a.qo_indptr[b] = run_tokens + et;
+      a.last[b] = L > 0 ? (L - 1) % kPage + 1 : kPage;
+      if (!a.new_lens) {
+        a.bi[b] = b;
+        a.pos[b] = L - 1;
+      }
+    }
+    run_pages += tot_p;
+    run_tokens += tot_t;
+  }
+  if (__syncthreads_or(clipped) && threadIdx.x == 0 && a.err) atomicAdd(a.err, 1);
+  if (threadIdx.x == 0) {
+    a.kv_indptr[a.batch] = run_pages;
+    if (a.qo_indptr) a.qo_indptr[a.batch] = run_tokens;
+  }
+}
+
+// Grid (x, b): the page ids of sequence b copied out of its table row, and
+// (prefill) its new tokens' sequence / position rows.  Entries past the
+// output capacities (or behind offsets that overflowed int32) are dropped and
+// counted once per sequence.
+__global__ void __launch_bounds__(256) meta_fill_kernel(MetaArgs a) {
+  const int b = blockIdx.y;
+  const int L = a.kv_lens[b];
+  const int np = seq_pages(a, L);
+  const int off = a.kv_indptr[b];
+  const int step = gridDim.x * blockDim.x;
+  const int first = blockIdx.x * blockDim.x + threadIdx.x;
+  const int32_t* row = a.tables + (int64_t)b * a.stride;
+  bool over = false;
+  for (int i = first; i < np; i += step) {
+    if (off >= 0 && (int64_t)off + i < a.indices_cap) a.kv_indices[off + i] = row[i];
+    else over = true;
+  }
+  if (a.new_lens) {
+    const int nt = seq_new_tokens(a, b, L);
+    const int qo = a.qo_indptr[b];
+    for (int j = first; j < nt; j += step) {
+      const int64_t t = (int64_t)qo + j;
+      if (qo >= 0 && t < a.tokens_cap) {
+        a.bi[t] = b;
+        a.pos[t] = L - nt + j;
+      } else {
+        over = true;
+      }
+    }
+  }
+  if (__syncthreads_or(over) && threadIdx.x == 0 && a.err) atomicAdd(a.err, 1);
+}
+
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" {
+
+int pagedattn_build_paged_metadata(const int32_t* block_tables, int64_t table_stride,
+                                   int32_t max_pages, const int32_t* kv_lens,
+                                   const int32_t* new_lens, int32_t batch_size,
+                                   int32_t* qo_indptr, int32_t* kv_indptr, int32_t* kv_indices,
+                                   int32_t indices_capacity, int32_t* kv_last_page_len,
+                                   int32_t* batch_indices, int32_t* positions,
+                                   int32_t tokens_capacity, int32_t* error_flag, void* stream) {
+  const char* who = "build_paged_metadata";
+  if (batch_size < 0 || max_pages < 0 || table_stride < max_pages || indices_capacity < 0 ||
+      tokens_capacity < 0)
+    return set_error(PAGEDATTN_ERR_INVALID,
+                     "%s: bad sizes batch=%d max_pages=%d stride=%lld capacities=%d/%d", who,
+                     batch_size, max_pages, (long long)table_stride, indices_capacity,
+                     tokens_capacity);
+  if (!kv_indptr || (batch_size > 0 && (!kv_lens || !kv_last_page_len || !batch_indices ||
+                                        !positions || (max_pages > 0 && !block_tables) ||
+                                        (indices_capacity > 0 && !kv_indices))))
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: null pointer", who);
+  if (new_lens && !qo_indptr)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: a prefill step (new_lens) needs qo_indptr",
+                     who);
+  if (!new_lens && tokens_capacity < batch_size)
+    return set_error(PAGEDATTN_ERR_INVALID,
+                     "%s: a decode step writes one token row per sequence (%d > capacity %d)",
+                     who, batch_size, tokens_capacity);
+  if (batch_size > 65535)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: batch_size %d above 65535", who,
+                     batch_size);
+  MetaArgs a{block_tables, table_stride, max_pages, kv_lens, new_lens, batch_size,
+             qo_indptr, kv_indptr, kv_indices, indices_capacity, kv_last_page_len,
+             batch_indices, positions, tokens_capacity, error_flag};
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(meta_scan_kernel, dim3(1), dim3(kMetaThreads), 0, s, a);
+  int rc = check_launch(who);
+  if (rc || batch_size == 0) return rc;
+  const unsigned gx = (unsigned)std::max(1, std::min(64, (max_pages + 255) / 256));
+  hipLaunchKernelGGL(meta_fill_kernel, dim3(gx, batch_size), dim3(256), 0, s, a);
+  return check_launch(who);
+}
+
+}  // extern "C"

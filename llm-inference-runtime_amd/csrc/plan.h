@@ -53,6 +53,9 @@ struct pagedattn_plan {
   int n_items = 0, n_merge = 0, n_slots = 0, split_pages = 0;
   // decode: log2 of the waves (KV heads) per head group
   int hg_shift = 0;
+  // decode: the partition is made on the device at run time from kv_indptr
+  // (n_items = number of shares); no work list in the workspace
+  bool implicit = false;
   // prefill: query tokens per tile (rows = tokens * hq/hkv)
   int q_tile = 0;
   int64_t total_qo = 0;

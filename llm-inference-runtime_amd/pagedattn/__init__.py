@@ -13,6 +13,7 @@ from .ops import (  # noqa: F401
     append_paged_kv_cache,
     append_paged_kv_cache_e4m3_amax,
     apply_rope_pos_ids_inplace,
+    build_paged_metadata,
     copy_bytes,
     fork_pages,
     get_batch_indices_positions,
@@ -28,6 +29,7 @@ __all__ = [
     "append_paged_kv_cache",
     "append_paged_kv_cache_e4m3_amax",
     "apply_rope_pos_ids_inplace",
+    "build_paged_metadata",
     "copy_bytes",
     "fork_pages",
     "get_batch_indices_positions",

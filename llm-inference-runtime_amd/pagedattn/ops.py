@@ -17,7 +17,8 @@ Only the "HND" pool layout the engine uses is implemented
 engine never passes (positional encoding inside attention, sliding windows,
 logit soft-capping, custom masks) raise NotImplementedError.
 
-Additions with no FlashInfer counterpart: ``quantize_pages_e4m3``, the
+Additions with no FlashInfer counterpart: ``build_paged_metadata`` (the
+step metadata built on the device), ``quantize_pages_e4m3``, the
 ``kv_scales`` argument for e4m3 pools with per-(page, K|V, kv-head) scales,
 ``append_paged_kv_cache_e4m3_amax`` (e4m3 append that maintains those
 scales as pages fill) and ``fork_pages`` (copy-on-write page fork).
@@ -26,6 +27,7 @@ scales as pages fill) and ``fork_pages`` (copy-on-write page fork).
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 
 import torch
 
@@ -349,6 +351,84 @@ def fork_pages(kv_pool: torch.Tensor, src_pages, dst_pages, valid_tokens=None,
          ptr(error_flag), _stream(device))
 
 
+@dataclass
+class PagedBuffers:
+    """Device metadata of one step, in the layout the attention calls take."""
+    qo_indptr: torch.Tensor        # [B + 1]
+    kv_indptr: torch.Tensor        # [B + 1]
+    kv_indices: torch.Tensor       # [capacity]
+    kv_last_page_len: torch.Tensor  # [B]
+    batch_indices: torch.Tensor    # [token capacity]
+    positions: torch.Tensor        # [token capacity]
+
+
+def new_paged_buffers(batch_size: int, indices_capacity: int, tokens_capacity: int,
+                      device) -> PagedBuffers:
+    """Fixed-capacity buffers for build_paged_metadata (a captured step keeps
+    reusing the same ones)."""
+    def z(n):
+        return torch.zeros(max(int(n), 1), dtype=torch.int32, device=device)[:int(n)]
+    return PagedBuffers(z(batch_size + 1), z(batch_size + 1), z(indices_capacity),
+                        z(batch_size), z(tokens_capacity), z(tokens_capacity))
+
+
+def build_paged_metadata(block_tables: torch.Tensor, kv_lens: torch.Tensor,
+                         new_lens: torch.Tensor | None = None, *,
+                         out: PagedBuffers | None = None,
+                         indices_capacity: int | None = None,
+                         tokens_capacity: int | None = None,
+                         error_flag: torch.Tensor | None = None) -> PagedBuffers:
+    """Step metadata built on the device from a block table [B, max_pages]
+    (int32, row b = sequence b's pages) and kv lengths [B] (tokens in the
+    cache once this step's tokens are appended).  The engine builds the same
+    lists in Python and uploads them every step
+    (src/engine/runtime/step_executor.py:98-165 prefill, :204-234 decode);
+    here nothing leaves the device:
+      kv_indptr / kv_indices: the first ceil(L/16) pages of every row
+        (decode too: the reference passes the whole row, which overstates
+        kv_len by a page when L % 16 == 0),
+      kv_last_page_len = L % 16 or 16,
+      qo_indptr: prefix sum of new_lens (decode: arange(B + 1)),
+      batch_indices / positions: each new token's sequence and position
+        (decode: row b = sequence b at L - 1; prefill: L - n .. L - 1).
+    With `out`, the results land in those buffers (fixed addresses for HIP
+    graph capture); otherwise new tensors sized for this call are returned.
+    Pages past a row's max_pages or outputs past a capacity are dropped and
+    counted in `error_flag`."""
+    _require_cuda(block_tables, "block_tables")
+    device = block_tables.device
+    if block_tables.dim() != 2 or block_tables.dtype != torch.int32 or \
+            block_tables.stride(1) != 1:
+        raise ValueError("block_tables must be an int32 [batch, max_pages] tensor with "
+                         "contiguous rows")
+    bsz, max_pages = block_tables.shape
+    for name, t in (("kv_lens", kv_lens), ("new_lens", new_lens)):
+        if t is None:
+            continue
+        _require_cuda(t, name)
+        if t.dtype != torch.int32 or t.numel() != bsz or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous int32 device tensor of {bsz} entries")
+    if out is None:
+        if indices_capacity is None:
+            indices_capacity = bsz * max_pages
+        if tokens_capacity is None:
+            tokens_capacity = bsz if new_lens is None else int(new_lens.sum().item())
+        out = new_paged_buffers(bsz, indices_capacity, tokens_capacity, device)
+    for name in ("qo_indptr", "kv_indptr"):
+        if getattr(out, name).numel() < bsz + 1:
+            raise ValueError(f"out.{name} holds fewer than {bsz + 1} entries")
+    if out.kv_last_page_len.numel() < bsz:
+        raise ValueError(f"out.kv_last_page_len holds fewer than {bsz} entries")
+    n_tok = min(out.batch_indices.numel(), out.positions.numel())
+    if error_flag is not None and (error_flag.dtype != torch.int32 or error_flag.numel() < 1):
+        raise ValueError("error_flag must be an int32 device tensor")
+    call("pagedattn_build_paged_metadata", ptr(block_tables), block_tables.stride(0), max_pages,
+         ptr(kv_lens), ptr(new_lens), bsz, ptr(out.qo_indptr), ptr(out.kv_indptr),
+         ptr(out.kv_indices), out.kv_indices.numel(), ptr(out.kv_last_page_len),
+         ptr(out.batch_indices), ptr(out.positions), n_tok, ptr(error_flag), _stream(device))
+    return out
+
+
 def quantize_pages_e4m3(pool: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """bf16/fp16 layer pool -> (e4m3 pool, fp32 scales [P, 2, Hkv]) with
     scale = amax / 448 per (page, K|V, kv-head) block (1.0 for an all-zero block)."""
@@ -399,13 +479,17 @@ def _unsupported_options(pos_encoding_mode="NONE", window_left=-1, logits_soft_c
 
 
 class _WrapperBase:
+    _graph_capable = False
+
     def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
                  use_cuda_graph: bool = False, **_unused):
         if kv_layout != "HND":
             raise NotImplementedError(
                 f"kv_layout {kv_layout!r}: only the HND page layout is implemented")
-        if use_cuda_graph:
-            raise NotImplementedError("use_cuda_graph wrappers are not implemented")
+        if use_cuda_graph and not self._graph_capable:
+            raise NotImplementedError(
+                f"use_cuda_graph is not implemented for {type(self).__name__}")
+        self._use_graph = bool(use_cuda_graph)
         _require_cuda(float_workspace_buffer, "float_workspace_buffer")
         if not float_workspace_buffer.is_contiguous():
             raise ValueError("the workspace must be contiguous")
@@ -432,7 +516,39 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
 
     Long sequences are split into KV chunks whose partials are merged by
     log-sum-exp; `plan(..., split_pages=n)` fixes the chunk size (pages),
-    0 lets the planner balance the work over the GPU, -1 disables splitting."""
+    0 lets the planner balance the work over the GPU, -1 disables splitting.
+
+    `plan(..., device_plan=True)` -- and every plan of a wrapper made with
+    use_cuda_graph=True -- reads nothing on the host: the attention launch
+    partitions the work itself from kv_indptr at run time (the same balanced
+    split), so a step can be replayed from a HIP graph while the metadata
+    changes in place.  With use_cuda_graph=True the run reads the metadata
+    from paged_kv_indptr_buffer / paged_kv_indices_buffer /
+    paged_kv_last_page_len_buffer (int32, fixed addresses); plan() copies
+    the tensors it is given into them unless they are those buffers."""
+
+    _graph_capable = True
+
+    def __init__(self, float_workspace_buffer: torch.Tensor, kv_layout: str = "NHD",
+                 use_cuda_graph: bool = False, use_tensor_cores: bool = False,
+                 paged_kv_indptr_buffer: torch.Tensor | None = None,
+                 paged_kv_indices_buffer: torch.Tensor | None = None,
+                 paged_kv_last_page_len_buffer: torch.Tensor | None = None, **kw):
+        super().__init__(float_workspace_buffer, kv_layout, use_cuda_graph, **kw)
+        self._graph_bufs = None
+        if use_cuda_graph:
+            bufs = (paged_kv_indptr_buffer, paged_kv_indices_buffer,
+                    paged_kv_last_page_len_buffer)
+            if any(b is None for b in bufs):
+                raise ValueError("use_cuda_graph needs paged_kv_indptr_buffer, "
+                                 "paged_kv_indices_buffer and paged_kv_last_page_len_buffer")
+            for b in bufs:
+                _require_cuda(b, "paged_kv buffer")
+                if b.dtype != torch.int32 or not b.is_contiguous():
+                    raise ValueError("the paged_kv buffers must be contiguous int32")
+            if paged_kv_indptr_buffer.numel() != paged_kv_last_page_len_buffer.numel() + 1:
+                raise ValueError("paged_kv_indptr_buffer must hold batch + 1 entries")
+            self._graph_bufs = bufs
 
     def plan(self, indptr: torch.Tensor, indices: torch.Tensor, last_page_len: torch.Tensor,
              num_qo_heads: int, num_kv_heads: int, head_dim: int, page_size: int,
@@ -440,10 +556,15 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
              logits_soft_cap: float | None = None, q_data_type="float16",
              kv_data_type=None, data_type=None, sm_scale: float | None = None,
              rope_scale=None, rope_theta=None, non_blocking: bool = True,
-             split_pages: int = 0, **_unused) -> None:
+             split_pages: int = 0, device_plan: bool = False, **_unused) -> None:
         _unsupported_options(pos_encoding_mode, window_left, logits_soft_cap)
         if page_size != PAGE_SIZE:
             raise NotImplementedError(f"page_size {page_size} (only 16 is implemented)")
+        if self._use_graph or device_plan:
+            self._plan_device(indptr, indices, last_page_len, num_qo_heads, num_kv_heads,
+                              head_dim, page_size, q_data_type, kv_data_type, data_type,
+                              sm_scale)
+            return
         device = self._ws.device
         indptr_h = _host_i32(indptr)
         last_h = _host_i32(last_page_len)
@@ -461,6 +582,36 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
         self._indptr = _i32(indptr, device)
         self._indices = _i32(indices, device)
         self._last = _i32(last_page_len, device)
+        self._bsz, self._hq, self._hkv, self._d = bsz, int(num_qo_heads), int(num_kv_heads), int(head_dim)
+        self._sm_scale = sm_scale
+        self._planned = True
+
+    def _plan_device(self, indptr, indices, last_page_len, num_qo_heads, num_kv_heads,
+                     head_dim, page_size, q_data_type, kv_data_type, data_type, sm_scale):
+        device = self._ws.device
+        bsz = last_page_len.numel()
+        if indptr.numel() != bsz + 1:
+            raise ValueError(f"indptr has {indptr.numel()} entries for {bsz} sequences")
+        if self._graph_bufs is not None:
+            b_indptr, b_indices, b_last = self._graph_bufs
+            if b_last.numel() != bsz:
+                raise ValueError(f"the graph buffers hold {b_last.numel()} sequences, "
+                                 f"the plan has {bsz}")
+            if indices.numel() > b_indices.numel():
+                raise ValueError("indices do not fit paged_kv_indices_buffer")
+            for src, dst in ((indptr, b_indptr), (last_page_len, b_last),
+                             (indices, b_indices[:indices.numel()])):
+                if src.data_ptr() != dst.data_ptr():
+                    dst.copy_(src, non_blocking=True)
+            self._indptr, self._indices, self._last = b_indptr, b_indices, b_last
+        else:
+            self._indptr = _i32(indptr, device)
+            self._indices = _i32(indices, device)
+            self._last = _i32(last_page_len, device)
+        self._q_dtype = _dtype_of(data_type if data_type is not None else q_data_type)
+        self._kv_dtype = _dtype_of(kv_data_type) if kv_data_type is not None else None
+        call("pagedattn_decode_plan_device", self._plan.handle, bsz, int(num_qo_heads),
+             int(num_kv_heads), int(head_dim), int(page_size), ptr(self._ws), self._ws_bytes)
         self._bsz, self._hq, self._hkv, self._d = bsz, int(num_qo_heads), int(num_kv_heads), int(head_dim)
         self._sm_scale = sm_scale
         self._planned = True
@@ -588,6 +739,36 @@ class BatchPrefillWithPagedKVCacheWrapper(_WrapperBase):
         self._bsz, self._hq, self._hkv, self._d = (bsz, int(num_qo_heads), int(num_kv_heads),
                                                    int(head_dim_qk))
         self._causal = bool(causal)
+        self._sm_scale = sm_scale
+        self._planned = True
+
+    def _plan_device(self, indptr, indices, last_page_len, num_qo_heads, num_kv_heads,
+                     head_dim, page_size, q_data_type, kv_data_type, data_type, sm_scale):
+        device = self._ws.device
+        bsz = last_page_len.numel()
+        if indptr.numel() != bsz + 1:
+            raise ValueError(f"indptr has {indptr.numel()} entries for {bsz} sequences")
+        if self._graph_bufs is not None:
+            b_indptr, b_indices, b_last = self._graph_bufs
+            if b_last.numel() != bsz:
+                raise ValueError(f"the graph buffers hold {b_last.numel()} sequences, "
+                                 f"the plan has {bsz}")
+            if indices.numel() > b_indices.numel():
+                raise ValueError("indices do not fit paged_kv_indices_buffer")
+            for src, dst in ((indptr, b_indptr), (last_page_len, b_last),
+                             (indices, b_indices[:indices.numel()])):
+                if src.data_ptr() != dst.data_ptr():
+                    dst.copy_(src, non_blocking=True)
+            self._indptr, self._indices, self._last = b_indptr, b_indices, b_last
+        else:
+            self._indptr = _i32(indptr, device)
+            self._indices = _i32(indices, device)
+            self._last = _i32(last_page_len, device)
+        self._q_dtype = _dtype_of(data_type if data_type is not None else q_data_type)
+        self._kv_dtype = _dtype_of(kv_data_type) if kv_data_type is not None else None
+        call("pagedattn_decode_plan_device", self._plan.handle, bsz, int(num_qo_heads),
+             int(num_kv_heads), int(head_dim), int(page_size), ptr(self._ws), self._ws_bytes)
+        self._bsz, self._hq, self._hkv, self._d = bsz, int(num_qo_heads), int(num_kv_heads), int(head_dim)
         self._sm_scale = sm_scale
         self._planned = True
 

@@ -1,0 +1,204 @@
+"""Device-side metadata and planner, and a decode step replayed from a HIP
+graph.
+
+* build_paged_metadata on the GPU equals the step executor's metadata rules
+  (pagedattn.metadata, bit-exact), for decode and chunked-prefill steps;
+* a device-planned decode equals the host-planned balanced split bit for bit
+  (same partition, same merge order) and the oracle within tolerance, for
+  empty, short, long and mixed batches;
+* a decode step (metadata build + RoPE + append + attention + merge)
+  captured once and replayed over several steps, with the lengths, the
+  inputs and the pool changing in place between replays, matches the same
+  step run eagerly, every replay."""
+
+import numpy as np
+import pytest
+import torch
+
+import pagedattn
+from pagedattn.metadata import decode_metadata, prefill_metadata
+
+from paged_cases import (decode_case, i32, lse_err, max_err, oracle_decode, random_tables,
+                         run_decode, workspace)
+
+pytestmark = pytest.mark.gpu
+
+
+def _tables_tensor(tables, max_pages, device, fill=-7):
+    t = np.full((len(tables), max_pages), fill, dtype=np.int32)
+    for b, row in enumerate(tables):
+        t[b, :len(row)] = row
+    return i32(t, device)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_build_paged_metadata_decode(gpu, seed):
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1, 700, size=57).tolist()
+    lens[3] = 16
+    lens[4] = 32  # page-aligned lengths: the table is cut, not passed whole
+    tables, _ = random_tables(rng, [n + 40 for n in lens])  # rows longer than needed
+    maxp = max(len(t) for t in tables)
+    bt = _tables_tensor(tables, maxp, gpu)
+    got = pagedattn.build_paged_metadata(bt, i32(lens, gpu))
+    want = decode_metadata(tables, lens)
+    assert np.array_equal(got.kv_indptr.cpu().numpy(), want.kv_indptr)
+    n = int(want.kv_indptr[-1])
+    assert np.array_equal(got.kv_indices[:n].cpu().numpy(), want.kv_indices)
+    assert np.array_equal(got.kv_last_page_len.cpu().numpy(), want.kv_last_page_len)
+    assert np.array_equal(got.qo_indptr.cpu().numpy(), want.qo_indptr)
+    assert np.array_equal(got.batch_indices.cpu().numpy(), want.batch_indices)
+    assert np.array_equal(got.positions.cpu().numpy(), want.positions)
+
+
+def test_build_paged_metadata_prefill(gpu):
+    rng = np.random.default_rng(2)
+    computed = [0, 16, 35, 100, 0, 7]
+    chunks = [17, 1, 64, 29, 0, 512]
+    lens = [c + n for c, n in zip(computed, chunks)]
+    tables, _ = random_tables(rng, [n + 20 for n in lens])
+    maxp = max(len(t) for t in tables)
+    bt = _tables_tensor(tables, maxp, gpu)
+    got = pagedattn.build_paged_metadata(bt, i32(lens, gpu), i32(chunks, gpu))
+    want = prefill_metadata(tables, computed, chunks)
+    for name in ("kv_indptr", "kv_last_page_len", "qo_indptr", "batch_indices", "positions"):
+        assert np.array_equal(getattr(got, name).cpu().numpy(), getattr(want, name)), name
+    n = int(want.kv_indptr[-1])
+    assert np.array_equal(got.kv_indices[:n].cpu().numpy(), want.kv_indices)
+
+
+def test_build_paged_metadata_overflow_is_counted(gpu):
+    tables = [[1, 2], [3, 4, 5]]
+    bt = _tables_tensor(tables, 3, gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    # sequence 0 needs 4 pages but its row has 3 columns; indices capacity 4 < 3 + 2
+    out = pagedattn.ops.new_paged_buffers(2, 4, 2, gpu)
+    pagedattn.build_paged_metadata(bt, i32([60, 20], gpu), out=out, error_flag=err)
+    assert out.kv_indptr.cpu().tolist() == [0, 3, 5]
+    assert out.kv_indices.cpu().tolist() == [1, 2, -7, 3]
+    assert int(err.item()) == 2
+
+
+def _device_plan_run(gpu, meta, pool, q, hq, hkv, d, kv_scales=None):
+    w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(workspace(gpu), "HND")
+    w.plan(i32(meta.kv_indptr, gpu), i32(meta.kv_indices, gpu), i32(meta.kv_last_page_len, gpu),
+           hq, hkv, d, 16, q_data_type=q.dtype, device_plan=True)
+    out, lse = w.run(q, pool, kv_scales=kv_scales, return_lse=True)
+    torch.cuda.synchronize()
+    return out, lse
+
+
+@pytest.mark.parametrize("name,lens,hq,hkv,d", [
+    ("tinyllama", list(np.random.default_rng(5).integers(256, 2049, 256)), 32, 4, 64),
+    ("long", [40000, 3, 70000, 16, 123457, 9000, 1, 17], 32, 8, 128),
+    ("empties", [0, 5, 0, 0, 300, 0], 32, 8, 128),
+    ("single", [1], 8, 8, 128),
+    ("mixed_g8", list(np.random.default_rng(6).integers(1, 9000, 40)), 64, 8, 128),
+])
+def test_device_plan_equals_host_plan(gpu, name, lens, hq, hkv, d):
+    lens = [int(x) for x in lens]
+    meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=len(lens))
+    got, got_lse = _device_plan_run(gpu, meta, pool, q, hq, hkv, d)
+    want, want_lse = run_decode(gpu, meta, pool, q, hq, hkv, d, split_pages=0)
+    assert torch.equal(got, want)
+    assert torch.equal(got_lse, want_lse)
+    rows = [b for b in range(len(lens)) if lens[b] <= 20000][:24]
+    ref, ref_lse = oracle_decode(meta, pool, q, batch=rows)
+    assert max_err(got, ref, rows) < 2e-2
+    assert lse_err(got_lse, ref_lse, rows) < 2e-2
+
+
+def test_device_plan_e4m3(gpu):
+    lens = [int(x) for x in np.random.default_rng(7).integers(1, 8192, 32)]
+    meta, pool, q = decode_case(gpu, lens, 64, 8, 128, seed=7)
+    q8, scales = pagedattn.quantize_pages_e4m3(pool)
+    got, got_lse = _device_plan_run(gpu, meta, q8, q, 64, 8, 128, kv_scales=scales)
+    want, want_lse = run_decode(gpu, meta, q8, q, 64, 8, 128, split_pages=0, kv_scales=scales)
+    assert torch.equal(got, want) and torch.equal(got_lse, want_lse)
+
+
+class _Step:
+    """One engine decode step on fixed buffers: metadata from the block table
+    and lengths, then RoPE + append + attention (+ merge) in the fused
+    launch."""
+
+    def __init__(self, gpu, tables, maxp, hq, hkv, d, graph):
+        self.bsz = len(tables)
+        self.bt = _tables_tensor(tables, maxp, gpu)
+        self.lens = torch.zeros(self.bsz, dtype=torch.int32, device=gpu)
+        self.buf = pagedattn.ops.new_paged_buffers(self.bsz, self.bsz * maxp, self.bsz, gpu)
+        self.q = torch.zeros((self.bsz, hq, d), dtype=torch.bfloat16, device=gpu)
+        self.k = torch.zeros((self.bsz, hkv, d), dtype=torch.bfloat16, device=gpu)
+        self.v = torch.zeros_like(self.k)
+        self.out = torch.zeros_like(self.q)
+        kw = {}
+        if graph:
+            kw = dict(use_cuda_graph=True, paged_kv_indptr_buffer=self.buf.kv_indptr,
+                      paged_kv_indices_buffer=self.buf.kv_indices,
+                      paged_kv_last_page_len_buffer=self.buf.kv_last_page_len)
+        self.w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(workspace(gpu), "HND", **kw)
+        self.w.plan(self.buf.kv_indptr, self.buf.kv_indices, self.buf.kv_last_page_len, hq, hkv,
+                    d, 16, q_data_type=torch.bfloat16, device_plan=True)
+
+    def __call__(self, pool):
+        pagedattn.build_paged_metadata(self.bt, self.lens, out=self.buf)
+        self.w.run(self.q, pool, out=self.out, append_key=self.k, append_value=self.v,
+                   rope=(1.0, 5e5), positions=self.buf.positions)
+
+
+def test_decode_step_graph_replay(gpu):
+    rng = np.random.default_rng(11)
+    hq, hkv, d = 32, 8, 128
+    start = [int(x) for x in rng.integers(1, 3000, 48)]
+    start[0], start[1] = 15, 16  # crosses a page boundary in the first replays
+    steps = 6
+    tables, num_pages = random_tables(rng, [n + steps for n in start], extra_pages=2)
+    maxp = max(len(t) for t in tables)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(11)
+    pool_g = torch.randn((num_pages, 2, hkv, 16, d), generator=g, device=gpu).to(torch.bfloat16)
+    pool_e = pool_g.clone()
+    eager = _Step(gpu, tables, maxp, hq, hkv, d, graph=False)
+    graphed = _Step(gpu, tables, maxp, hq, hkv, d, graph=True)
+    lens0 = torch.tensor(start, dtype=torch.int32, device=gpu)
+    graphed.lens.copy_(lens0)
+    # warm up on a side stream, as torch asks before a capture
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    scratch = pool_g.clone()
+    with torch.cuda.stream(s):
+        graphed(scratch)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    del scratch
+    cg = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cg):
+        graphed(pool_g)
+    lens = lens0.clone()
+    for step in range(steps):
+        lens += 1  # each step appends one token per sequence
+        for st in (eager, graphed):
+            st.lens.copy_(lens)
+        q = torch.randn((len(start), hq, d), generator=g, device=gpu).to(torch.bfloat16)
+        k = torch.randn((len(start), hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+        v = torch.randn((len(start), hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+        for st in (eager, graphed):
+            st.q.copy_(q)
+            st.k.copy_(k)
+            st.v.copy_(v)
+        cg.replay()
+        eager(pool_e)
+        torch.cuda.synchronize()
+        assert torch.equal(graphed.out, eager.out), step
+        assert torch.equal(pool_g, pool_e), step
+        assert torch.equal(graphed.buf.positions, lens - 1)
+    # and the eager step itself follows the oracle on the final state
+    meta = decode_metadata(tables, lens.cpu().tolist())
+    rows = list(range(0, len(start), 4))
+    qr = eager.q.clone()
+    # the fused launch rotated q in registers only: rotate a copy for the oracle
+    from pagedattn import ops
+    ops.apply_rope_pos_ids_inplace(qr, torch.zeros_like(eager.k), i32(meta.positions, gpu),
+                                   rope_scale=1.0, rope_theta=5e5)
+    ref, _ = oracle_decode(meta, pool_e, qr, batch=rows)
+    assert max_err(eager.out, ref, rows) < 2e-2
