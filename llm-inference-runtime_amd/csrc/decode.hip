@@ -288,6 +288,8 @@ __device__ __forceinline__ void load_pair(Stage<D, BF16, FP8>& st,
   }
 }
 
+constexpr float kDecodeRescaleSlack = 8.f;
+
 template <int D, bool BF16, bool FP8>
 struct SoftmaxState {
   f32x4 o[D / 16];
@@ -298,119 +300,144 @@ struct SoftmaxState {
 // the bits stored in the pool (e4m3 pools: quantised with the page's scale):
 // K row at byte 0, V row at byte D * ESZ.  Only the pair holding the new
 // token reads it, so it costs no registers in the main loop.
-// patch_pi >= 0: page half patch_pi of this pair holds the token appended in
-// this launch at `slot`; its stale loaded values are replaced by the new row
-// with per-lane selects where they are used.
-template <int D, bool BF16, bool FP8>
-__device__ __forceinline__ void compute_pair(const Stage<D, BF16, FP8>& st,
-                                             const u32x4 (&qf)[D / 32],
-                                             SoftmaxState<D, BF16, FP8>& sm,
-                                             float scale_log2, int G, int n,
-                                             const uint8_t* new_row,
-                                             int patch_pi, int slot) {
+// One call handles NPC page pairs (one register stage) as one online-softmax
+// step: one cross-lane max and one rescale check for all of them, and their
+// independent MFMA chains interleave.  patch_k >= 0: page half patch_pi of
+// pair patch_k holds the token appended in this launch at `slot`; its stale
+// loaded values are replaced by the new row where they are used.
+template <int D, bool BF16, bool FP8, int NPC>
+__device__ __forceinline__ void compute_pairs(const Stage<D, BF16, FP8> (&st)[NPC],
+                                              const u32x4 (&qf)[D / 32],
+                                              SoftmaxState<D, BF16, FP8>& sm,
+                                              float scale_log2, int G, int n,
+                                              const uint8_t* new_row, int patch_k,
+                                              int patch_pi, int slot) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
-  // ---- S^T = K . Q^T for both pages
-  f32x4 s4[2];
+  constexpr int NS = NPC * 8;  // scores per lane
+  // ---- S^T = K . Q^T for every page of the stage
+  f32x4 s4[NPC][2];
 #pragma unroll
-  for (int pi = 0; pi < 2; ++pi) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < NPC; ++k)
 #pragma unroll
-    for (int ks = 0; ks < Tr::KS; ++ks) {
-      typename Tr::KRaw kr = st.k[pi][ks];
-      if (patch_pi == pi) {
-        const auto nk = *reinterpret_cast<const typename Tr::KRaw*>(
-            new_row + (32 * ks + 8 * G) * Tr::ESZ);
-        if (n == slot) kr = nk;
+    for (int pi = 0; pi < 2; ++pi) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < Tr::KS; ++ks) {
+        typename Tr::KRaw kr = st[k].k[pi][ks];
+        if (patch_k == k && patch_pi == pi) {
+          const auto nk = *reinterpret_cast<const typename Tr::KRaw*>(
+              new_row + (32 * ks + 8 * G) * Tr::ESZ);
+          if (n == slot) kr = nk;
+        }
+        u32x4 a;
+        if constexpr (FP8) {
+          a = e4m3x8_to_16<BF16>(kr[0], kr[1]);
+        } else {
+          a = kr;
+        }
+        acc = mfma16<BF16>(a, qf[ks], acc);
       }
-      u32x4 a;
-      if constexpr (FP8) {
-        a = e4m3x8_to_16<BF16>(kr[0], kr[1]);
-      } else {
-        a = kr;
-      }
-      acc = mfma16<BF16>(a, qf[ks], acc);
+      s4[k][pi] = acc;
     }
-    s4[pi] = acc;
+  float s[NS];
+  bool partial = false;
+#pragma unroll
+  for (int k = 0; k < NPC; ++k)
+#pragma unroll
+    for (int pi = 0; pi < 2; ++pi) {
+      const float c = FP8 ? scale_log2 * st[k].kscale[pi] : scale_log2;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[k * 8 + pi * 4 + r] = s4[k][pi][r] * c;
+      partial |= st[k].ntok[pi] < kPage;
+    }
+  if (partial) {
+#pragma unroll
+    for (int k = 0; k < NPC; ++k)
+#pragma unroll
+      for (int pi = 0; pi < 2; ++pi)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (4 * G + r >= st[k].ntok[pi]) s[k * 8 + pi * 4 + r] = -INFINITY;
   }
-  float s[8];
-#pragma unroll
-  for (int pi = 0; pi < 2; ++pi) {
-    const float c = FP8 ? scale_log2 * st.kscale[pi] : scale_log2;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) s[pi * 4 + r] = s4[pi][r] * c;
-  }
-  if (st.ntok[0] < kPage || st.ntok[1] < kPage) {
-#pragma unroll
-    for (int pi = 0; pi < 2; ++pi)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (4 * G + r >= st.ntok[pi]) s[pi * 4 + r] = -INFINITY;
-  }
-  // ---- online softmax (all 8 values of a lane belong to its head)
+  // ---- online softmax (all values of a lane belong to its head), lazy:
+  // the running max only moves, with a rescale of O and l, when a score
+  // exceeds it by more than kDecodeRescaleSlack (log2 units), so P stays
+  // <= 2^slack and most steps skip the rescale.  exp2 is the raw v_exp_f32.
   float mx = s[0];
 #pragma unroll
-  for (int j = 1; j < 8; ++j) mx = fmaxf(mx, s[j]);
+  for (int j = 1; j < NS; ++j) mx = fmaxf(mx, s[j]);
   mx = max_over_groups16(mx);
-  const float m_new = fmaxf(sm.m, mx);
-  const float m_use = m_new == -INFINITY ? 0.f : m_new;
-  const float alpha = exp2f(sm.m - m_use);
-  float pr[8];
+  const bool grow = mx > sm.m + kDecodeRescaleSlack;
+  if (__builtin_amdgcn_ballot_w64(grow)) {
+    const float m_new = grow ? mx : sm.m;
+    const float alpha = __builtin_amdgcn_exp2f(sm.m - m_new);
+    sm.l *= alpha;
+#pragma unroll
+    for (int e = 0; e < W; ++e) sm.o[e] *= alpha;
+    sm.m = m_new;
+  }
+  const float m_use = sm.m == -INFINITY ? 0.f : sm.m;
+  float pr[NS];
   float psum = 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    pr[j] = exp2f(s[j] - m_use);
+  for (int j = 0; j < NS; ++j) {
+    pr[j] = __builtin_amdgcn_exp2f(s[j] - m_use);
     psum += pr[j];
   }
-  sm.l = sm.l * alpha + psum;
-  sm.m = m_new;
+  sm.l += psum;
 #pragma unroll
-  for (int e = 0; e < W; ++e) sm.o[e] *= alpha;
-  if constexpr (FP8) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) pr[j] *= st.vscale[j >> 2];
-  }
-  u32x4 pb;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) pb[i] = pack2<BF16>(pr[2 * i], pr[2 * i + 1]);
-  // ---- V rows as 16-bit values: lane holds W consecutive d per token
-  uint32_t vw[8][W / 2];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    typename Tr::VRaw vr = st.v[j];
-    if (patch_pi == (j >> 2)) {
-      const auto nv = *reinterpret_cast<const typename Tr::VRaw*>(
-          new_row + (D + W * n) * Tr::ESZ);
-      if (G == (slot >> 2) && (j & 3) == (slot & 3)) vr = nv;
-    }
+  for (int k = 0; k < NPC; ++k) {
     if constexpr (FP8) {
-      if constexpr (W == 8) {
-        const u32x4 c = e4m3x8_to_16<BF16>(dword_of(vr, 0),
-                                           dword_of(vr, 1));
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vw[j][i] = c[i];
-      } else {
-        const u32x2 c = e4m3x4_to_16<BF16>(dword_of(vr, 0));
-        vw[j][0] = c[0];
-        vw[j][1] = c[1];
+      for (int j = 0; j < 8; ++j) pr[k * 8 + j] *= st[k].vscale[j >> 2];
+    }
+    u32x4 pb;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pb[i] = pack2<BF16>(pr[k * 8 + 2 * i], pr[k * 8 + 2 * i + 1]);
+    // ---- V rows, tokens 2i and 2i+1 interleaved per d with one v_perm: the
+    // MFMA operand of tile row d = W m + e holds (token 2i, token 2i+1) at d.
+    constexpr int VWORDS = Tr::VB / 4;  // dwords of one token's V slice
+    uint32_t vw[8][VWORDS];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      typename Tr::VRaw vr = st[k].v[j];
+      if (patch_k == k && patch_pi == (j >> 2)) {
+        const auto nv = *reinterpret_cast<const typename Tr::VRaw*>(
+            new_row + (D + W * n) * Tr::ESZ);
+        if (G == (slot >> 2) && (j & 3) == (slot & 3)) vr = nv;
+      }
+#pragma unroll
+      for (int w = 0; w < VWORDS; ++w) vw[j][w] = dword_of(vr, w);
+    }
+    // ---- O^T += V^T . P^T, one MFMA per d offset e (tile rows d = W m + e)
+    if constexpr (FP8) {
+      // e4m3 bytes of d = e, e + 1 for tokens 2i, 2i+1 gathered into one
+      // dword; one converter per d gives the bf16 pair directly
+#pragma unroll
+      for (int e = 0; e < W; e += 2) {
+        u32x4 a0, a1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t t = __builtin_amdgcn_perm(vw[2 * i + 1][e >> 2], vw[2 * i][e >> 2],
+                                                   (e & 2) ? 0x07030602u : 0x05010400u);
+          a0[i] = e4m3x2_to_16<BF16, false>(t);
+          a1[i] = e4m3x2_to_16<BF16, true>(t);
+        }
+        sm.o[e] = mfma16<BF16>(a0, pb, sm.o[e]);
+        sm.o[e + 1] = mfma16<BF16>(a1, pb, sm.o[e + 1]);
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < W / 2; ++i) vw[j][i] = dword_of(vr, i);
-    }
-  }
-  // ---- O^T += V^T . P^T, one MFMA per d offset e (tile rows d = W m + e)
+      for (int e = 0; e < W; ++e) {
+        u32x4 a;
 #pragma unroll
-  for (int e = 0; e < W; ++e) {
-    u32x4 a;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t x0 = vw[2 * i][e >> 1];
-      const uint32_t x1 = vw[2 * i + 1][e >> 1];
-      a[i] = (e & 1) ? ((x0 >> 16) | (x1 & 0xffff0000u))
-                     : ((x0 & 0xffffu) | (x1 << 16));
+        for (int i = 0; i < 4; ++i)
+          a[i] = __builtin_amdgcn_perm(vw[2 * i + 1][e >> 1], vw[2 * i][e >> 1],
+                                       (e & 1) ? 0x07060302u : 0x05040100u);
+        sm.o[e] = mfma16<BF16>(a, pb, sm.o[e]);
+      }
     }
-    sm.o[e] = mfma16<BF16>(a, pb, sm.o[e]);
   }
 }
 
@@ -588,18 +615,19 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
       for (int k = 0; k < NP; ++k)
         load_pair(st[k], p, h, ids[k], page_lo + 2 * (NP * c + k), npages, last, n, G);
     };
+    // pairs past the end of the item were loaded as empty pages (no tokens,
+    // zero data) and add nothing
     auto compute_chunk = [&](Stage<D, BF16, FP8> (&st)[NP], int c) {
-#pragma unroll
-      for (int k = 0; k < NP; ++k) {
-        const int pr = NP * c + k;
-        if (pr >= n_pairs) break;
-        int patch_pi = -1;
-        if constexpr (APPEND) {
-          const int d_pg = new_pg - (page_lo + 2 * pr);
-          if (new_pg >= 0 && d_pg >= 0 && d_pg < 2) patch_pi = d_pg;
+      int patch_k = -1, patch_pi = -1;
+      if constexpr (APPEND) {
+        const int d_pg = new_pg - (page_lo + 2 * NP * c);
+        if (new_pg >= 0 && d_pg >= 0 && d_pg < 2 * NP) {
+          patch_k = d_pg >> 1;
+          patch_pi = d_pg & 1;
         }
-        compute_pair(st[k], qf, sm, p.scale_log2, G, n, new_row, patch_pi, new_slot);
       }
+      compute_pairs<D, BF16, FP8, NP>(st, qf, sm, p.scale_log2, G, n, new_row, patch_k,
+                                      patch_pi, new_slot);
     };
     if (n_chunks > 0) {
       Stage<D, BF16, FP8> sa[NP], sb[NP];
