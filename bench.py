@@ -176,6 +176,179 @@ def bench_prefill(w, args, dev, dtype, label):
     return res
 
 
+def _time_ms(fn, steps: int, warmup: int) -> float:
+    import torch
+    for i in range(warmup):
+        fn(i)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        fn(warmup + i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def _time_graph_ms(fn, steps: int, warmup: int) -> float:
+    """Device time per call of fn: `steps` calls captured in one HIP graph,
+    replayed and timed, so the host's per-call argument checks (tens of us
+    for a small launch) stay out of the figure."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(warmup):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
+    """The same fused decode step with the device-side partition
+    (pagedattn_decode_plan_device), eagerly and replayed from a HIP graph,
+    and the device metadata builder for the batch."""
+    import numpy as np
+    import torch
+
+    import pagedattn
+    from pagedattn import workloads as W
+
+    alg_step = W.decode_bytes(w, 2, with_append=True)
+    reps = _replicas(w.num_pages * 2 * w.hkv * 16 * w.d * 2)
+    inst = [W.materialize(w, dev, dtype, seed=w.seed * 100 + r) for r in range(reps)]
+    ws = torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
+    out = torch.empty((w.meta.batch_size, w.hq, w.d), dtype=dtype, device=dev)
+    t0 = inst[0]
+    dw = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    dw.plan(t0.kv_indptr, t0.kv_indices, t0.kv_last_page_len, w.hq, w.hkv, w.d, 16,
+            q_data_type=dtype, device_plan=True)
+
+    def step(t):
+        dw.run(t.q, t.pool, out=out, append_key=t.k_new, append_value=t.v_new)
+
+    eager_ms = _time_ms(lambda i: step(inst[i % reps]), steps, warmup)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for t in inst:
+            step(t)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graphs = []
+    for t in inst:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(t)
+        graphs.append(g)
+    graph_ms = _time_ms(lambda i: graphs[i % reps].replay(), steps, warmup)
+    # metadata of the batch from a block table on the device
+    m = w.meta
+    npg = np.diff(m.kv_indptr)
+    tables = np.full((m.batch_size, int(npg.max())), -1, dtype=np.int32)
+    for b in range(m.batch_size):
+        tables[b, :npg[b]] = m.kv_indices[m.kv_indptr[b]:m.kv_indptr[b + 1]]
+    bt = torch.from_numpy(tables).to(dev)
+    lens = torch.from_numpy(m.seq_lens.astype(np.int32)).to(dev)
+    buf = pagedattn.ops.new_paged_buffers(m.batch_size, tables.size, m.batch_size, dev)
+    meta_ms = _time_graph_ms(lambda i: pagedattn.build_paged_metadata(bt, lens, out=buf),
+                             steps, warmup)
+    del graphs, inst
+    torch.cuda.empty_cache()
+    return {"eager_ms_per_step": eager_ms, "eager_GBps": alg_step / (eager_ms * 1e-3) / 1e9,
+            "graph_ms_per_step": graph_ms, "graph_GBps": alg_step / (graph_ms * 1e-3) / 1e9,
+            "metadata_build_ms": meta_ms}
+
+
+def bench_kv_write(dev, steps: int = 20, warmup: int = 3) -> dict:
+    """The engine's KV write path: e4m3 append that keeps running-amax page
+    scales (a 4096-token prefill chunk of a Llama-3-70B layer, 8 KV heads,
+    D=128; and a 128-sequence decode step of that layer, timed for its
+    latency), and a copy-on-write fork of 256 pages across every layer of a
+    Llama-3-8B pool (32 layers, 8 KV heads, D=128, bf16).  Both move bytes
+    only: GB/s of algorithmic bytes (read + written)."""
+    import numpy as np
+    import torch
+
+    import pagedattn
+    from pagedattn.metadata import prefill_metadata
+
+    rng = np.random.default_rng(7)
+    hkv, d = 8, 128
+    # 4 sequences x 1024 new tokens after prefixes of 0..8191 tokens
+    computed = [int(x) // 16 * 16 for x in rng.integers(0, 8192, 4)]
+    chunks = [1024] * 4
+    need = [(c + n + 15) // 16 for c, n in zip(computed, chunks)]
+    perm = rng.permutation(sum(need) + 16)
+    tables, at = [], 0
+    for k in need:
+        tables.append(perm[at:at + k].tolist())
+        at += k
+    meta = prefill_metadata(tables, computed, chunks)
+    num_pages = len(perm)
+    q8 = torch.zeros((num_pages, 2, hkv, 16, d), dtype=torch.uint8,
+                     device=dev).view(torch.float8_e4m3fn)
+    scales = torch.zeros((num_pages, 2, hkv), dtype=torch.float32, device=dev)
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    k = torch.randn((meta.nnz, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn((meta.nnz, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    i32 = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.int32)).to(dev)
+    bi, pos, ind, indptr, last = (i32(meta.batch_indices), i32(meta.positions),
+                                  i32(meta.kv_indices), i32(meta.kv_indptr),
+                                  i32(meta.kv_last_page_len))
+    app_ms = _time_graph_ms(lambda i: pagedattn.append_paged_kv_cache_e4m3_amax(
+        k, v, bi, pos, q8, ind, indptr, last, scales, kv_layout="HND"), steps, warmup)
+    app_bytes = meta.nnz * hkv * d * 2 * (2 + 1)  # bf16 rows in, e4m3 rows out
+    # a decode step of the same layer: 128 sequences, one token each
+    from pagedattn.metadata import decode_metadata
+    lens = [int(x) for x in rng.integers(1, 8192, 128)]
+    need = [(n + 15) // 16 for n in lens]
+    perm = rng.permutation(sum(need))
+    tables, at = [], 0
+    for n_p in need:
+        tables.append(perm[at:at + n_p].tolist())
+        at += n_p
+    dm = decode_metadata(tables, lens)
+    q8d = torch.zeros((len(perm), 2, hkv, 16, d), dtype=torch.uint8,
+                      device=dev).view(torch.float8_e4m3fn)
+    sd = torch.zeros((len(perm), 2, hkv), dtype=torch.float32, device=dev)
+    kd = torch.randn((dm.nnz, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    vd = torch.randn((dm.nnz, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    dargs = (i32(dm.batch_indices), i32(dm.positions), q8d, i32(dm.kv_indices),
+             i32(dm.kv_indptr), i32(dm.kv_last_page_len), sd)
+    dec_ms = _time_graph_ms(lambda i: pagedattn.append_paged_kv_cache_e4m3_amax(
+        kd, vd, *dargs, kv_layout="HND"), steps, warmup)
+    layers, pages, n_fork = 32, 1024, 256
+    pool = torch.zeros((layers, pages, 2, hkv, 16, d), dtype=torch.bfloat16, device=dev)
+    src = rng.choice(pages // 2, n_fork, replace=False)
+    dst = pages // 2 + rng.choice(pages // 2, n_fork, replace=False)
+    src_d, dst_d = i32(src), i32(dst)
+    fork_ms = _time_graph_ms(lambda i: pagedattn.fork_pages(pool, src_d, dst_d), steps, warmup)
+    fork_bytes = n_fork * layers * 2 * hkv * 16 * d * 2 * 2  # read + write
+    del pool
+    torch.cuda.empty_cache()
+    return {"append_e4m3_amax": {"tokens": meta.nnz, "ms": app_ms,
+                                 "GBps": app_bytes / (app_ms * 1e-3) / 1e9},
+            "append_e4m3_amax.decode": {"tokens": dm.nnz, "ms": dec_ms},
+            "fork_pages": {"forks": n_fork, "layers": layers, "ms": fork_ms,
+                           "GBps": fork_bytes / (fork_ms * 1e-3) / 1e9}}
+
+
 def cpu_decode_baseline(w, t, n_seq: int, kv_elem: int):
     """fp32 oracle decode over the first n_seq sequences, timed on the host."""
     import numpy as np
@@ -324,6 +497,16 @@ def main() -> int:
                                           "alg_bytes_attn", "batch", "kv_tokens")},
             "prefill": p5,
         }
+        dp = bench_device_plan(main_w, dev, dtype)
+        log(f"tinyllama_decode (device plan): eager {dp['eager_ms_per_step']:.4f} ms, "
+            f"HIP graph replay {dp['graph_ms_per_step']:.4f} ms; metadata build "
+            f"{1e3 * dp['metadata_build_ms']:.1f} us")
+        extra["tinyllama_decode.device_plan"] = dp
+        kw = bench_kv_write(dev)
+        log(f"kv write path: e4m3 running-amax append {kw['append_e4m3_amax']['GBps']:.0f} GB/s "
+            f"(4096-token chunk), {1e3 * kw['append_e4m3_amax.decode']['ms']:.1f} us per "
+            f"128-token decode step; CoW fork {kw['fork_pages']['GBps']:.0f} GB/s")
+        extra["kv_write"] = kw
     cal = copy_calibration(dev)
     traffic = load_traffic()
     log(f"copy calibration: {cal['GBps']:.0f} GB/s (read+write)")

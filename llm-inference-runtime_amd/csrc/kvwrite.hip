@@ -6,6 +6,8 @@
 //    pages across every layer of the pool (todo.md:17-19 of the reference
 //    asks for it before a sequence appends to a shared partial block).
 // Both are HBM-bound byte movers; neither reads a byte twice from HBM.
+#include <algorithm>
+
 #include "append.h"
 
 namespace pa {
@@ -42,105 +44,151 @@ __device__ __forceinline__ u32x2 f32x8_to_e4m3(const float (&f)[8]) {
   return o;
 }
 
-// Token t continues token t - 1 inside one page: same sequence, next
-// position, not the first slot of a page.
-__device__ __forceinline__ bool continues_run(const AppendArgs& a, int t) {
-  const int b0 = load_invariant(a.batch_indices + t - 1);
-  const int b1 = load_invariant(a.batch_indices + t);
-  const int p0 = load_invariant(a.positions + t - 1);
-  const int p1 = load_invariant(a.positions + t);
-  return b0 == b1 && (int64_t)p1 == (int64_t)p0 + 1 && (p1 % kPage) != 0;
+// Token t starts a run: the tokens of one sequence that land in one page,
+// consecutive and in position order.  t starts one unless it continues
+// t - 1 (same sequence, next position, not the first slot of a page).
+__device__ __forceinline__ bool starts_run(const AppendArgs& a, int t) {
+  if (t <= 0 || t >= a.nnz) return true;
+  const int b0 = a.batch_indices[t - 1];
+  const int b1 = a.batch_indices[t];
+  const int p0 = a.positions[t - 1];
+  const int p1 = a.positions[t];
+  return !(b0 == b1 && (int64_t)p1 == (int64_t)p0 + 1 && (p1 % kPage) != 0);
 }
 
-constexpr int kAmaxMaxD = 256;                             // head_dim limit
-constexpr int kAmaxChunks = kPage * (kAmaxMaxD / 8) / kWave;  // 8-element chunks per lane
+constexpr int kAmaxMaxD = 256;  // head_dim limit
 
-// One wave per (token, K|V, kv-head).  The wave of the first token of a run
-// (tokens of one sequence that land in one page, in position order) owns the
-// run's (page, K|V, head) block; every other wave exits at once.
+// One run's (page, K|V, head) block, worked by the lanes of `width` lanes
+// (a power of two, a multiple of L = D/8): lane chunk gl of rows
+// row0, row0 + step, ... (NR rows at most).  Per run:
 //   s_old = scale if the run starts past slot 0, else 0
 //   s_new = max(s_old, pow2_scale(amax of the run's rows))
 //   s_new > s_old: rows [0, slot0) <- e4m3(decode(row) * (s_old / s_new))
-//   run rows <- e4m3(clamp(x / s_new, +-448))   (zero codes when s_new == 0)
-template <bool IS_BF16>
-__global__ void __launch_bounds__(256)
-    append_e4m3_amax_kernel(AppendArgs a, float* __restrict__ scales) {
-  const int wave = uniform(threadIdx.x >> 6);
-  const int lane = threadIdx.x & (kWave - 1);
-  const int units = 2 * a.hkv;
-  const int64_t w = (int64_t)blockIdx.x * 4 + wave;
-  if (w >= (int64_t)a.nnz * units) return;
-  const int t0 = uniform((int)(w / units));
-  const int kind = uniform((int)((w % units) / a.hkv));
-  const int h = uniform((int)(w % a.hkv));
-  if (t0 > 0 && continues_run(a, t0)) return;
-  int t1 = t0 + 1;
-  while (t1 < a.nnz && t1 - t0 < kPage && continues_run(a, t1)) ++t1;
-  const int n = t1 - t0;
+//   run rows <- e4m3(clamp(x * (1 / s_new), +-448))   (zero codes when s_new
+//   is 0; 1 / s_new is exact, s_new being a power of two in [2^-126, 2^127])
+template <bool IS_BF16, int NR>
+__device__ __forceinline__ void amax_run(const AppendArgs& a, float* __restrict__ scales,
+                                         const uint16_t* src, int64_t sn, int t0, int n,
+                                         int kind, int h, int gl, int row0, int step,
+                                         int width, bool leader) {
+  // every load in flight at once: rows past the run repeat its last row,
+  // which leaves the amax unchanged and is never written
+  u32x4 x[NR];
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+    const int j = min(row0 + k * step, n - 1);
+    x[k] = *reinterpret_cast<const u32x4*>(src + (int64_t)(t0 + j) * sn + 8 * gl);
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int k = 0; k < NR; ++k) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      amax = fmaxf(amax, fabsf(h2f<IS_BF16>((uint16_t)(x[k][e] & 0xffffu))));
+      amax = fmaxf(amax, fabsf(h2f<IS_BF16>((uint16_t)(x[k][e] >> 16))));
+    }
+  }
+  for (int off = width >> 1; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
   int slot0 = 0;
   const int64_t page = append_target_page(a, t0, &slot0);
   if (page < 0) {
-    if (lane == 0 && kind == 0 && h == 0 && a.err) atomicAdd(a.err, n);
+    if (leader && kind == 0 && h == 0 && a.err) atomicAdd(a.err, n);
     return;
   }
-  const int cpr = a.d >> 3;  // 8-element chunks per row
-  const int n_new = n * cpr;
-  const uint16_t* src = kind ? a.v + (int64_t)h * a.v_sh : a.k + (int64_t)h * a.k_sh;
-  const int64_t sn = kind ? a.v_sn : a.k_sn;
-
-  u32x4 x[kAmaxChunks];
-  float amax = 0.f;
-#pragma unroll
-  for (int i = 0; i < kAmaxChunks; ++i) {
-    const int c = lane + kWave * i;
-    x[i] = u32x4{0u, 0u, 0u, 0u};
-    if (c < n_new) {
-      const int row = c / cpr;
-      x[i] = *reinterpret_cast<const u32x4*>(src + (int64_t)(t0 + row) * sn + 8 * (c % cpr));
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        amax = fmaxf(amax, fabsf(h2f<IS_BF16>((uint16_t)(x[i][e] & 0xffffu))));
-        amax = fmaxf(amax, fabsf(h2f<IS_BF16>((uint16_t)(x[i][e] >> 16))));
-      }
-    }
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
-
   const int64_t sidx = (page * 2 + kind) * a.hkv + h;
   const float s_old = slot0 > 0 ? scales[sidx] : 0.f;
   const float s_new = fmaxf(s_old, pow2_scale_of(amax));
   uint8_t* blk = static_cast<uint8_t*>(a.cache) + sidx * kPage * (int64_t)a.d;
-
   if (slot0 > 0 && s_new > s_old) {
-    const float r = s_old / s_new;
-    for (int c = lane; c < slot0 * cpr; c += kWave) {
+    const float ratio = s_old / s_new;
+    for (int row = row0; row < slot0; row += step) {
+      uint8_t* q = blk + (int64_t)row * a.d + 8 * gl;
       float f[8];
-      e4m3x8_to_f32(*reinterpret_cast<const u32x2*>(blk + 8 * c), f);
+      e4m3x8_to_f32(*reinterpret_cast<const u32x2*>(q), f);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] * r, -448.f), 448.f);
-      *reinterpret_cast<u32x2*>(blk + 8 * c) = f32x8_to_e4m3(f);
+      for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] * ratio, -448.f), 448.f);
+      *reinterpret_cast<u32x2*>(q) = f32x8_to_e4m3(f);
     }
   }
+  const float inv = s_new > 0.f ? 1.f / s_new : 0.f;
 #pragma unroll
-  for (int i = 0; i < kAmaxChunks; ++i) {
-    const int c = lane + kWave * i;
-    if (c >= n_new) continue;
+  for (int k = 0; k < NR; ++k) {
+    const int j = row0 + k * step;
+    if (j >= n) continue;
     u32x2 o = {0u, 0u};
     if (s_new > 0.f) {
       float f[8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        f[2 * e] = h2f<IS_BF16>((uint16_t)(x[i][e] & 0xffffu));
-        f[2 * e + 1] = h2f<IS_BF16>((uint16_t)(x[i][e] >> 16));
+        f[2 * e] = h2f<IS_BF16>((uint16_t)(x[k][e] & 0xffffu));
+        f[2 * e + 1] = h2f<IS_BF16>((uint16_t)(x[k][e] >> 16));
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / s_new, -448.f), 448.f);
+      for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] * inv, -448.f), 448.f);
       o = f32x8_to_e4m3(f);
     }
-    *reinterpret_cast<u32x2*>(blk + (int64_t)slot0 * a.d + 8 * c) = o;
+    *reinterpret_cast<u32x2*>(blk + (int64_t)(slot0 + j) * a.d + 8 * gl) = o;
   }
-  if (lane == 0) scales[sidx] = s_new;
+  if (leader) scales[sidx] = s_new;
+}
+
+// One wave per (block of `blk` <= 16 tokens, K|V, kv-head), four waves to a
+// workgroup.  Lanes test 32 tokens for run starts (a run is at most 16
+// tokens, so every run that starts in the block ends inside the window).
+// Lane groups of L = D/8 lanes hold one 8-element chunk of a row per lane;
+// ngroups = 64 / L groups to a wave.
+//   RPL == 0 (decode-like steps, blk = min(16, ngroups), about one token per
+//     run): the runs starting in the block go round-robin to the groups, one
+//     run's 16 rows per group;
+//   RPL > 0 (prefill chunks, blk = 16, about one run per block): the whole
+//     wave works one run at a time, group g taking rows g, g + ngroups, ...
+//     (RPL = 16 / ngroups rows per lane).
+template <bool IS_BF16, int RPL>
+__global__ void __launch_bounds__(256)
+    append_e4m3_amax_kernel(AppendArgs a, float* __restrict__ scales, int nblk) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int kh_count = 2 * a.hkv;
+  if (w >= ((int64_t)a.nnz + nblk - 1) / nblk * kh_count) return;
+  const int t_blk = uniform((int)(w / kh_count)) * nblk;
+  const int kind = uniform((int)(w % kh_count)) / a.hkv;
+  const int h = uniform((int)(w % kh_count)) % a.hkv;
+  const int L = a.d >> 3;       // lanes per row
+  const int ngroups = kWave / L;
+  const int grp = lane / L;
+  const int gl = lane % L;      // chunk of the row this lane moves
+  const uint64_t starts = __builtin_amdgcn_ballot_w64(lane < 32 && starts_run(a, t_blk + lane));
+  const uint32_t in_blk = (uint32_t)starts & ((1u << nblk) - 1u);
+  const int n_runs = __builtin_popcount(in_blk);
+  const uint16_t* src = kind ? a.v + (int64_t)h * a.v_sh : a.k + (int64_t)h * a.k_sh;
+  const int64_t sn = kind ? a.v_sn : a.k_sn;
+  // the r-th run start of the block, and the run's length
+  auto run_of = [&](int r, int* t0, int* n) {
+    uint32_t m = in_blk;
+    for (int i = 0; i < r; ++i) m &= m - 1;
+    const int i0 = __builtin_ctz(m);
+    const uint64_t after = (starts >> (i0 + 1)) | (1ull << (31 - i0));
+    *t0 = t_blk + i0;
+    *n = min((int)__builtin_ctzll(after) + 1, a.nnz - *t0);
+  };
+  if constexpr (RPL == 0) {
+    for (int r0 = 0; r0 < n_runs; r0 += ngroups) {
+      const int r = r0 + grp;
+      if (r >= n_runs) continue;
+      int t0, n;
+      run_of(r, &t0, &n);
+      if (t0 >= a.nnz) continue;
+      amax_run<IS_BF16, kPage>(a, scales, src, sn, t0, n, kind, h, gl, 0, 1, L, gl == 0);
+    }
+  } else {
+    for (int r = 0; r < n_runs; ++r) {
+      int t0, n;
+      run_of(r, &t0, &n);
+      if (t0 >= a.nnz) continue;
+      amax_run<IS_BF16, RPL>(a, scales, src, sn, t0, n, kind, h, gl, grp, ngroups, kWave,
+                             lane == 0);
+    }
+  }
 }
 
 // ----------------------------------------------------------------------------
@@ -205,8 +253,10 @@ int pagedattn_append_paged_kv_cache_e4m3_amax(
     int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int32_t* error_flag,
     void* stream) {
   const char* who = "append_paged_kv_cache_e4m3_amax";
-  if (head_dim > kAmaxMaxD)
-    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: head_dim %d above %d", who, head_dim,
+  // one 8-element chunk per lane, a row on a power-of-two group of lanes
+  if (head_dim > kAmaxMaxD || head_dim < 8 || (head_dim & (head_dim - 1)))
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                     "%s: head_dim %d must be a power of two in [8, %d]", who, head_dim,
                      kAmaxMaxD);
   AppendArgs a;
   bool empty = false;
@@ -216,18 +266,27 @@ int pagedattn_append_paged_kv_cache_e4m3_amax(
                         kv_indptr, batch_size, num_kv_heads, head_dim, page_size, error_flag,
                         &a, &empty);
   if (rc || empty) return rc;
-  const int64_t waves = (int64_t)nnz * 2 * num_kv_heads;
-  const int64_t blocks = (waves + 3) / 4;
-  if (blocks > INT32_MAX)
-    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: %lld tokens x heads is too many", who,
-                     (long long)waves);
+  // decode-like steps (under 4 new tokens per sequence on average): one run
+  // per lane group; else 16-token blocks, each worked by the whole wave
+  const int ngroups = 64 / (head_dim / 8);
+  const bool per_group = (int64_t)nnz < 4 * (int64_t)std::max(batch_size, 1);
+  const int blk = per_group ? std::min(ngroups, 16) : 16;
+  const int rpl = std::max(1, 16 / ngroups);
+  const int64_t waves = ((int64_t)nnz + blk - 1) / blk * 2 * num_kv_heads;
+  if ((waves + 3) / 4 > INT32_MAX)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: %d tokens x %d heads is too many", who,
+                     nnz, num_kv_heads);
+  const dim3 grid((unsigned)((waves + 3) / 4));
   hipStream_t s = (hipStream_t)stream;
-  if (src_dtype == PAGEDATTN_BF16)
-    hipLaunchKernelGGL(append_e4m3_amax_kernel<true>, dim3((unsigned)blocks), dim3(256), 0,
-                       s, a, kv_scales);
-  else
-    hipLaunchKernelGGL(append_e4m3_amax_kernel<false>, dim3((unsigned)blocks), dim3(256), 0,
-                       s, a, kv_scales);
+  const bool bf16 = src_dtype == PAGEDATTN_BF16;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, a, kv_scales, blk);
+  };
+  if (per_group) launch(bf16 ? append_e4m3_amax_kernel<true, 0> : append_e4m3_amax_kernel<false, 0>);
+  else if (rpl == 8) launch(bf16 ? append_e4m3_amax_kernel<true, 8> : append_e4m3_amax_kernel<false, 8>);
+  else if (rpl == 4) launch(bf16 ? append_e4m3_amax_kernel<true, 4> : append_e4m3_amax_kernel<false, 4>);
+  else if (rpl == 2) launch(bf16 ? append_e4m3_amax_kernel<true, 2> : append_e4m3_amax_kernel<false, 2>);
+  else launch(bf16 ? append_e4m3_amax_kernel<true, 1> : append_e4m3_amax_kernel<false, 1>);
   return check_launch(who);
 }
 

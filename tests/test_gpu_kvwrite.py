@@ -33,7 +33,7 @@ def _amax_append(gpu, meta, q8, scales, k, v, err=None, bi=None, pos=None):
 
 
 @pytest.mark.parametrize("src", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("d", [64, 128, 256])
 def test_amax_append_prefill_then_decode(gpu, src, d):
     rng = np.random.default_rng(10 + d)
     hkv = 4
