@@ -877,6 +877,17 @@ static int decode_waves_per_cu() {
   return 4;
 }
 
+// Page-equivalents charged per item by the balanced split (the cost of an
+// item switch, measured: 6 gave the fastest TinyLlama B=256 step, 60.5 us
+// against 63.7 us at 0); PAGEDATTN_DECODE_ITEM_COST overrides it.
+static int decode_item_cost() {
+  if (const char* env = std::getenv("PAGEDATTN_DECODE_ITEM_COST")) {
+    const int v = std::atoi(env);
+    if (v >= 0 && v <= 1024) return v;
+  }
+  return 6;
+}
+
 // Waves (KV heads) per head group: the largest of 4, 2, 1 that divides Hkv,
 // so a page's K and V blocks are each read as one run of hg * 16 rows;
 // PAGEDATTN_DECODE_HEAD_GROUP (1, 2 or 4) caps it.
@@ -983,32 +994,52 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
       wave_ptr.push_back((int32_t)items.size());
     }
   } else {
-    // balanced: the (sequence, head group, page) stream cut into equal shares
-    int64_t target = (total * ngrp + groups_max - 1) / groups_max;
-    target = std::max<int64_t>(4, (target + 1) / 2 * 2);
-    int64_t fill = 0;
-    for (int b = 0; b < batch_size; ++b)
-      for (int hgrp = 0; hgrp < ngrp; ++hgrp) {
-        if (npages[b] == 0) {
-          items.push_back(make(b, hgrp, 0, 0));
-          pieces[(size_t)b * ngrp + hgrp]++;
-          continue;
-        }
-        int lo = 0;
-        while (lo < npages[b]) {
-          const int take = (int)std::min<int64_t>(npages[b] - lo, target - fill);
-          items.push_back(make(b, hgrp, lo, lo + take));
-          pieces[(size_t)b * ngrp + hgrp]++;
-          lo += take;
-          fill += take;
-          if (fill == target) {
-            wave_ptr.push_back((int32_t)items.size());
-            fill = 0;
+    // balanced: the (sequence, head group, page) stream cut into equal
+    // shares.  A share is counted in pages plus `cost` page-equivalents per
+    // item it holds, since every item start waits for a fresh round trip of
+    // loads: a share of several short pieces gets fewer pages and the groups
+    // finish together.  Shares are contiguous, so only a group's first and
+    // last items can be pieces of cut sequences.
+    const int64_t cost = decode_item_cost();
+    const int64_t est_items = (int64_t)batch_size * ngrp + groups_max;
+    int64_t target = (total * ngrp + cost * est_items + groups_max - 1) / groups_max;
+    target = std::max<int64_t>(4 + cost, (target + 1) / 2 * 2);
+    for (;;) {
+      items.clear();
+      wave_ptr.assign(1, 0);
+      std::fill(pieces.begin(), pieces.end(), 0);
+      int64_t fill = 0;
+      for (int b = 0; b < batch_size; ++b)
+        for (int hgrp = 0; hgrp < ngrp; ++hgrp) {
+          if (npages[b] == 0) {
+            items.push_back(make(b, hgrp, 0, 0));
+            pieces[(size_t)b * ngrp + hgrp]++;
+            continue;
+          }
+          int lo = 0;
+          while (lo < npages[b]) {
+            if (fill > 0 && fill + cost >= target) {
+              wave_ptr.push_back((int32_t)items.size());
+              fill = 0;
+            }
+            const int take = (int)std::min<int64_t>(npages[b] - lo, target - fill - cost);
+            items.push_back(make(b, hgrp, lo, lo + take));
+            pieces[(size_t)b * ngrp + hgrp]++;
+            lo += take;
+            fill += take + cost;
+            if (fill >= target) {
+              wave_ptr.push_back((int32_t)items.size());
+              fill = 0;
+            }
           }
         }
-      }
-    if (wave_ptr.back() != (int32_t)items.size())
-      wave_ptr.push_back((int32_t)items.size());
+      if (wave_ptr.back() != (int32_t)items.size())
+        wave_ptr.push_back((int32_t)items.size());
+      // the item charge can overshoot the estimate: never more shares than
+      // head groups the launch keeps resident
+      if ((int64_t)wave_ptr.size() - 1 <= groups_max || cost == 0) break;
+      target += 2;
+    }
   }
 
   // Partial slots and merge groups for (sequence, head group) pairs cut in

@@ -51,6 +51,20 @@ def test_decode_head_groups(gpu, monkeypatch, head_group, hq, hkv):
         assert lse_err(lse, ref_l) <= TOL_LSE, split
 
 
+@pytest.mark.parametrize("cost", ["0", "6", "40"])
+def test_decode_balanced_item_cost(gpu, monkeypatch, cost):
+    # the balanced split charges page-equivalents per item (shares of many
+    # short pieces get fewer pages); any charge is still a partition of the
+    # (sequence, head group, page) stream and gives the oracle's answer
+    monkeypatch.setenv("PAGEDATTN_DECODE_ITEM_COST", cost)
+    lens = EDGE_LENS + [int(x) for x in np.random.default_rng(3).integers(1, 3000, 60)]
+    meta, pool, q = decode_case(gpu, lens, 32, 8, 128, seed=13)
+    ref_o, ref_l = oracle_decode(meta, pool, q)
+    out, lse = run_decode(gpu, meta, pool, q, 32, 8, 128, split_pages=0)
+    assert max_err(out, ref_o) <= TOL_BF16
+    assert lse_err(lse, ref_l) <= TOL_LSE
+
+
 def test_decode_fp16(gpu):
     meta, pool, q = decode_case(gpu, EDGE_LENS, 32, 4, 64, dtype=torch.float16, seed=11)
     ref_o, ref_l = oracle_decode(meta, pool, q)

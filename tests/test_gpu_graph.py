@@ -95,7 +95,10 @@ def _device_plan_run(gpu, meta, pool, q, hq, hkv, d, kv_scales=None):
     ("single", [1], 8, 8, 128),
     ("mixed_g8", list(np.random.default_rng(6).integers(1, 9000, 40)), 64, 8, 128),
 ])
-def test_device_plan_equals_host_plan(gpu, name, lens, hq, hkv, d):
+def test_device_plan_equals_host_plan(gpu, name, lens, hq, hkv, d, monkeypatch):
+    # the device partition cuts equal page shares; the host planner's
+    # balanced split does the same with no per-item charge
+    monkeypatch.setenv("PAGEDATTN_DECODE_ITEM_COST", "0")
     lens = [int(x) for x in lens]
     meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=len(lens))
     got, got_lse = _device_plan_run(gpu, meta, pool, q, hq, hkv, d)
@@ -108,7 +111,8 @@ def test_device_plan_equals_host_plan(gpu, name, lens, hq, hkv, d):
     assert lse_err(got_lse, ref_lse, rows) < 2e-2
 
 
-def test_device_plan_e4m3(gpu):
+def test_device_plan_e4m3(gpu, monkeypatch):
+    monkeypatch.setenv("PAGEDATTN_DECODE_ITEM_COST", "0")
     lens = [int(x) for x in np.random.default_rng(7).integers(1, 8192, 32)]
     meta, pool, q = decode_case(gpu, lens, 64, 8, 128, seed=7)
     q8, scales = pagedattn.quantize_pages_e4m3(pool)
