@@ -49,6 +49,7 @@ struct DecodeParams {
   const int32_t* wave_ptr;  // [n_groups + 1]: items of head group w
   int32_t n_groups, n_merge, n_slots, batch_size;
   int32_t hg_shift;  // log2(waves per head group), 0..2
+  int32_t item_cost;  // implicit partition: header units per segment
   const uint16_t* q;
   int64_t q_sn, q_sh;
   const uint8_t* cache;
@@ -194,39 +195,50 @@ struct Stage {
 // Page ids of a pair, fetched with scalar loads two pairs ahead of use
 // (-1: absent or invalid page).
 // Device-side decode partition (plans made with pagedattn_decode_plan_device):
-// stream = (pages of all sequences) x (head groups per sequence), cut into
-// shares of `share` pages, share >= 4 and even, with at most n_groups shares.
-// The same rule as the host planner's balanced split.
+// a virtual stream of (sequence, head group) segments in sequence-major
+// order, segment (b, hgrp) being `cost` header units followed by the
+// sequence's pages, cut into shares of `share` units (share >= 4 + cost and
+// even, at most n_groups shares).  The headers charge each item start, as
+// the host planner's balanced split does; with cost 0 the two partitions
+// are the same.  Segment (b, hgrp) starts at
+//   seg(b) + hgrp * (np_b + cost),
+//   seg(b) = ngrp * (kv_indptr[b] - kv_indptr[0]) + cost * ngrp * b,
+// and its page j sits at unit start + cost + j.
 struct ImplicitSplit {
   int64_t stream, share;
-  int base, ngrp;
+  int base, ngrp, cost;
 };
 
 __device__ __forceinline__ ImplicitSplit implicit_split(const int32_t* kv_indptr, int batch,
-                                                        int ngrp, int n_groups) {
+                                                        int ngrp, int n_groups, int cost) {
   ImplicitSplit sp;
   sp.ngrp = ngrp;
+  sp.cost = cost;
   sp.base = uniform(load_invariant(kv_indptr));
   const int top = uniform(load_invariant(kv_indptr + batch));
-  sp.stream = (int64_t)ngrp * max(0, top - sp.base);
+  sp.stream = (int64_t)ngrp * max(0, top - sp.base) + (int64_t)cost * ngrp * batch;
   int64_t t = (sp.stream + n_groups - 1) / n_groups;
   t = (t + 1) / 2 * 2;
-  sp.share = max<int64_t>(4, t);
+  sp.share = max<int64_t>(4 + cost, t);
   return sp;
 }
 
-// Largest b in [0, batch) with ngrp * (kv_indptr[b] - base) <= x, by a
+__device__ __forceinline__ int64_t seq_start(const ImplicitSplit& sp, int b, int ind_lo) {
+  return (int64_t)sp.ngrp * (ind_lo - sp.base) + (int64_t)sp.cost * sp.ngrp * b;
+}
+
+// Largest b in [0, batch) whose segments start at or before unit x, by a
 // 64-way search: each round every lane tests one candidate of the range and
 // the ballot narrows it 64-fold.  Always ends (the range shrinks every
 // round) and stays in [0, batch) whatever kv_indptr holds.
-__device__ __forceinline__ int find_sequence(const int32_t* kv_indptr, int batch, int ngrp,
-                                             int base, int64_t x, int lane) {
+__device__ __forceinline__ int find_sequence(const int32_t* kv_indptr, int batch,
+                                             const ImplicitSplit& sp, int64_t x, int lane) {
   int lo = 0, hi = batch;
   while (hi - lo > 1) {
     const int step = (hi - lo + kWave - 1) / kWave;
     const int c = lo + lane * step;
     bool ok = false;
-    if (c < hi) ok = (int64_t)ngrp * (kv_indptr[c] - base) <= x;
+    if (c < hi) ok = seq_start(sp, c, kv_indptr[c]) <= x;
     const int cnt = __builtin_popcountll(__builtin_amdgcn_ballot_w64(ok));
     const int nlo = lo + max(cnt - 1, 0) * step;
     hi = uniform(min(nlo + step, hi));
@@ -705,22 +717,24 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
       run_item(b, h0, item_lo, item_hi, slot0);
     }
   } else {
-    // Device-side partition, read from kv_indptr at run time: the stream of
-    // (sequence, head group, page) triples in sequence-major order is cut
-    // into equal shares of T pages, share gw for head group gw.  A sequence
-    // cut by a share boundary leaves at most two pieces in one share (its
-    // first and its last item); they write slots 2 gw and 2 gw + 1.
+    // Device-side partition, read from kv_indptr at run time: the virtual
+    // stream of (sequence, head group) segments (implicit_split) is cut into
+    // equal shares, share gw for head group gw.  A sequence cut by a share
+    // boundary leaves at most two pieces in one share: one that continues
+    // from the previous share (slot 2 gw) and one that starts at the
+    // sequence's first page after the share's start (slot 2 gw + 1); a
+    // share's only piece may be both kinds and uses slot 2 gw.
     const ImplicitSplit sp = implicit_split(p.kv_indptr, p.batch_size, p.hkv >> p.hg_shift,
-                                            p.n_groups);
+                                            p.n_groups, p.item_cost);
     const int64_t start = (int64_t)gw * sp.share;
     if (start >= sp.stream) return;
     const int64_t end = min(start + sp.share, sp.stream);
     const int ngrp = sp.ngrp;
-    int b = find_sequence(p.kv_indptr, p.batch_size, ngrp, sp.base, start, lane);
+    int b = find_sequence(p.kv_indptr, p.batch_size, sp, start, lane);
     int ind_lo = uniform(load_invariant(p.kv_indptr + b));
     int np = uniform(load_invariant(p.kv_indptr + b + 1)) - ind_lo;
-    int hgrp = np > 0 ? (int)min<int64_t>(ngrp, max<int64_t>(0, (start - (int64_t)ngrp *
-                                                                          (ind_lo - sp.base)) / np))
+    int hgrp = np > 0 ? (int)min<int64_t>(ngrp, max<int64_t>(0, (start - seq_start(sp, b, ind_lo)) /
+                                                                      (np + sp.cost)))
                       : ngrp;
     int64_t pos = start;
     while (pos < end) {
@@ -731,14 +745,16 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
         hgrp = np > 0 ? 0 : ngrp;
         continue;
       }
-      const int64_t s_off = (int64_t)ngrp * (ind_lo - sp.base) + (int64_t)hgrp * np;
-      const int64_t lo = max<int64_t>(0, pos - s_off);
-      const int64_t hi = min<int64_t>(np, end - s_off);
+      // unit of the segment's first page; segments only move further on
+      const int64_t p0 = seq_start(sp, b, ind_lo) + (int64_t)hgrp * (np + sp.cost) + sp.cost;
+      if (p0 >= end) break;
+      const int64_t lo = max<int64_t>(0, pos - p0);
+      const int64_t hi = min<int64_t>(np, end - p0);
       if (hi > lo) {
         const bool cut = lo > 0 || hi < np;
-        const int slot0 = cut ? (2 * gw + (pos == start ? 0 : 1)) << p.hg_shift : -1;
+        const int slot0 = cut ? (2 * gw + ((lo == 0 && p0 > start) ? 1 : 0)) << p.hg_shift : -1;
         run_item(b, hgrp << p.hg_shift, (int)lo, (int)hi, slot0);
-        pos = s_off + hi;
+        pos = p0 + hi;
       }
       ++hgrp;
     }
@@ -792,7 +808,7 @@ struct MergeImplicitArgs {
   const float* pl;
   uint16_t* out;
   float* lse;
-  int32_t batch, hq, hkv, g, d, hg_shift, n_groups;
+  int32_t batch, hq, hkv, g, d, hg_shift, n_groups, item_cost;
 };
 
 template <bool BF16>
@@ -803,7 +819,7 @@ __global__ void __launch_bounds__(128) decode_merge_implicit_kernel(MergeImplici
   const int dd = threadIdx.x;
   const int head = h * a.g + hn;
   const int ngrp = a.hkv >> a.hg_shift;
-  const ImplicitSplit sp = implicit_split(a.kv_indptr, a.batch, ngrp, a.n_groups);
+  const ImplicitSplit sp = implicit_split(a.kv_indptr, a.batch, ngrp, a.n_groups, a.item_cost);
   const int ind_lo = load_invariant(a.kv_indptr + b);
   const int np = load_invariant(a.kv_indptr + b + 1) - ind_lo;
   uint16_t* orow = a.out + ((int64_t)b * a.hq + head) * a.d;
@@ -812,13 +828,15 @@ __global__ void __launch_bounds__(128) decode_merge_implicit_kernel(MergeImplici
     if (a.lse && dd == 0) a.lse[(int64_t)b * a.hq + head] = -INFINITY;
     return;
   }
-  const int64_t s_off = (int64_t)ngrp * (ind_lo - sp.base) + (int64_t)(h >> a.hg_shift) * np;
-  const int64_t first = s_off / sp.share;
-  const int64_t last = (s_off + np - 1) / sp.share;
-  if (s_off < 0 || first == last || last >= a.n_groups) return;
+  // unit of the segment's first page (implicit_split)
+  const int64_t p0 =
+      seq_start(sp, b, ind_lo) + (int64_t)(h >> a.hg_shift) * (np + sp.cost) + sp.cost;
+  const int64_t first = p0 / sp.share;
+  const int64_t last = (p0 + np - 1) / sp.share;
+  if (p0 < 0 || first == last || last >= a.n_groups) return;
   const int wi = h & ((1 << a.hg_shift) - 1);
   auto slot_of = [&](int64_t w) {
-    const int j = (w == first && s_off != w * sp.share) ? 1 : 0;
+    const int j = (w == first && p0 != w * sp.share) ? 1 : 0;
     return ((2 * w + j) << a.hg_shift) + wi;
   };
   float M = -INFINITY;
@@ -1150,6 +1168,7 @@ int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
   plan->workspace = workspace;
   plan->workspace_bytes = workspace_bytes;
   plan->implicit = true;
+  plan->item_cost = decode_item_cost();
   plan->batch_size = batch_size;
   plan->hq = num_qo_heads;
   plan->hkv = num_kv_heads;
@@ -1227,6 +1246,7 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   p.wave_ptr = plan->wave_ptr_dev;
   p.n_groups = plan->n_items;
   p.hg_shift = plan->hg_shift;
+  p.item_cost = plan->item_cost;
   p.n_merge = plan->n_merge;
   p.n_slots = plan->n_slots;
   p.batch_size = plan->batch_size;
@@ -1269,7 +1289,7 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   if (plan->implicit) {
     MergeImplicitArgs m{kv_indptr, plan->partial_o, plan->partial_lse, p.out, lse,
                         plan->batch_size, plan->hq, plan->hkv, p.g, plan->d,
-                        plan->hg_shift, plan->n_items};
+                        plan->hg_shift, plan->n_items, plan->item_cost};
     const dim3 grid((unsigned)((int64_t)plan->batch_size * plan->hkv), p.g);
     if (bf16)
       hipLaunchKernelGGL(decode_merge_implicit_kernel<true>, grid, dim3(plan->d), 0, s, m);

@@ -56,6 +56,9 @@ struct pagedattn_plan {
   // decode: the partition is made on the device at run time from kv_indptr
   // (n_items = number of shares); no work list in the workspace
   bool implicit = false;
+  // decode, implicit: page-equivalents charged per (sequence, head group)
+  // segment by the device-side split
+  int item_cost = 0;
   // prefill: query tokens per tile (rows = tokens * hq/hkv)
   int q_tile = 0;
   int64_t total_qo = 0;

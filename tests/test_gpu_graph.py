@@ -111,6 +111,28 @@ def test_device_plan_equals_host_plan(gpu, name, lens, hq, hkv, d, monkeypatch):
     assert lse_err(got_lse, ref_lse, rows) < 2e-2
 
 
+@pytest.mark.parametrize("cost", ["6", "40"])
+@pytest.mark.parametrize("name,lens,hq,hkv,d", [
+    ("tinyllama", list(np.random.default_rng(5).integers(256, 2049, 256)), 32, 4, 64),
+    ("empties", [0, 5, 0, 0, 300, 0, 17, 0], 32, 8, 128),
+    ("mixed_g8", list(np.random.default_rng(6).integers(1, 9000, 40)), 64, 8, 128),
+])
+def test_device_plan_item_cost(gpu, monkeypatch, cost, name, lens, hq, hkv, d):
+    # the device split with a per-segment charge (header units before each
+    # (sequence, head group) segment) is still a partition: oracle answer,
+    # and the host plan's answer to the rounding of the merges
+    monkeypatch.setenv("PAGEDATTN_DECODE_ITEM_COST", cost)
+    lens = [int(x) for x in lens]
+    meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=len(lens) + 1)
+    got, got_lse = _device_plan_run(gpu, meta, pool, q, hq, hkv, d)
+    want, want_lse = run_decode(gpu, meta, pool, q, hq, hkv, d, split_pages=0)
+    assert float((got.float() - want.float()).abs().max()) <= 1e-2
+    rows = [b for b in range(len(lens)) if lens[b] <= 20000][:24]
+    ref, ref_lse = oracle_decode(meta, pool, q, batch=rows)
+    assert max_err(got, ref, rows) < 2e-2
+    assert lse_err(got_lse, ref_lse, rows) < 2e-2
+
+
 def test_device_plan_e4m3(gpu, monkeypatch):
     monkeypatch.setenv("PAGEDATTN_DECODE_ITEM_COST", "0")
     lens = [int(x) for x in np.random.default_rng(7).integers(1, 8192, 32)]
