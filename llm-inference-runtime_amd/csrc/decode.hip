@@ -761,6 +761,48 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
   }
 }
 
+// Combine the base-2 partials of n pieces, slot_of(s) giving piece s's
+// (slot * g + head) index: M = max lse, den = sum 2^(lse - M), num = sum
+// 2^(lse - M) o[dd].  The lse and o of up to four pieces are loaded together,
+// so the o loads do not wait for the max; later batches rescale the sums.
+template <typename SlotOf>
+__device__ __forceinline__ void merge_pieces(int n, SlotOf slot_of, const float* __restrict__ pl,
+                                             const float* __restrict__ po, int d, int dd,
+                                             float* M_out, float* num_out, float* den_out) {
+  constexpr int kBatch = 4;
+  float M = -INFINITY, num = 0.f, den = 0.f;
+  for (int s0 = 0; s0 < n; s0 += kBatch) {
+    float lv[kBatch], ov[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      lv[k] = -INFINITY;
+      ov[k] = 0.f;
+      if (s0 + k < n) {
+        const int64_t sh = slot_of(s0 + k);
+        lv[k] = pl[sh];
+        if (dd < d) ov[k] = po[sh * d + dd];
+      }
+    }
+    float Mb = M;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) Mb = fmaxf(Mb, lv[k]);
+    if (Mb == -INFINITY) continue;
+    const float r = M == -INFINITY ? 0.f : exp2f(M - Mb);
+    num *= r;
+    den *= r;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const float wt = lv[k] == -INFINITY ? 0.f : exp2f(lv[k] - Mb);
+      den += wt;
+      num += wt * ov[k];
+    }
+    M = Mb;
+  }
+  *M_out = M;
+  *num_out = num;
+  *den_out = den;
+}
+
 // Split-KV merge, one workgroup per (split group, query head):
 // o = sum_c 2^(lse_c - M) o_c / sum_c 2^(lse_c - M),
 // lse = M + log2(sum_c 2^(lse_c - M)) (base-2 partials, natural-log output).
@@ -775,19 +817,10 @@ __global__ void __launch_bounds__(128)
   const MergeItem mi = merges[blockIdx.x];
   const int hn = blockIdx.y;  // query head within the group
   const int head = mi.h * g + hn;
-  float M = -INFINITY;
-  for (int s = 0; s < mi.nslots; ++s)
-    M = fmaxf(M, pl[(int64_t)(mi.slot0 + s * mi.stride) * g + hn]);
-  float num = 0.f, den = 0.f;
   const int dd = threadIdx.x;
-  if (M != -INFINITY) {
-    for (int s = 0; s < mi.nslots; ++s) {
-      const int64_t sh = (int64_t)(mi.slot0 + s * mi.stride) * g + hn;
-      const float wt = exp2f(pl[sh] - M);
-      den += wt;
-      if (dd < d) num += wt * po[sh * d + dd];
-    }
-  }
+  float M, num, den;
+  merge_pieces(mi.nslots, [&](int s) { return (int64_t)(mi.slot0 + s * mi.stride) * g + hn; },
+               pl, po, d, dd, &M, &num, &den);
   if (dd < d)
     out[((int64_t)mi.b * hq + head) * d + dd] =
         f2h<BF16>(M != -INFINITY ? num / den : 0.f);
@@ -839,17 +872,9 @@ __global__ void __launch_bounds__(128) decode_merge_implicit_kernel(MergeImplici
     const int j = (w == first && p0 != w * sp.share) ? 1 : 0;
     return ((2 * w + j) << a.hg_shift) + wi;
   };
-  float M = -INFINITY;
-  for (int64_t w = first; w <= last; ++w) M = fmaxf(M, a.pl[slot_of(w) * a.g + hn]);
-  float num = 0.f, den = 0.f;
-  if (M != -INFINITY) {
-    for (int64_t w = first; w <= last; ++w) {
-      const int64_t sh = slot_of(w) * a.g + hn;
-      const float wt = exp2f(a.pl[sh] - M);
-      den += wt;
-      if (dd < a.d) num += wt * a.po[sh * a.d + dd];
-    }
-  }
+  float M, num, den;
+  merge_pieces((int)(last - first + 1), [&](int s) { return slot_of(first + s) * a.g + hn; },
+               a.pl, a.po, a.d, dd, &M, &num, &den);
   if (dd < a.d) orow[dd] = f2h<BF16>(M != -INFINITY ? num / den : 0.f);
   if (a.lse && dd == 0)
     a.lse[(int64_t)b * a.hq + head] =
