@@ -106,14 +106,22 @@ struct PrefillCfg {
 };
 
 // Chunk swizzle of LDS row r: chunk c of the row is stored at position
-// c ^ swz(r).  D = 128 (16 chunks of 16 B per row): 16 consecutive rows get
-// 16 distinct positions for one chunk (K operand reads, one chunk per lane
-// and row), and 4 consecutive rows never collide for a chunk pair {2i,
-// 2i + 1} (V transpose reads).  D = 64 (8 chunks): the same with 8 rows.
+// c ^ swz(r).  LDS has 64 banks of 4 bytes, so a 16-byte position p of a
+// 256-byte row covers banks 4p..4p+3.  D = 128 (16 chunks of 16 B per row):
+//  * K operand reads (ds_read_b128; 16 lanes at a time read one chunk of 16
+//    consecutive rows) need swz to be a bijection on r mod 16;
+//  * V transpose reads (ds_read_b64_tr_b16; 32 lanes at a time read chunks
+//    4i..4i+3 of 4 consecutive rows) need the 4 rows to put that chunk
+//    quad in 4 different position quads, i.e. distinct swz(r) >> 2.
+// Swapping the two 2-bit fields of r mod 16 does both: no bank conflicts for
+// either read (measured with SQ_LDS_BANK_CONFLICT; the previous
+// ((r & 7) << 1) | ((r >> 3) & 1) left the transpose reads 2-way
+// conflicted, half their LDS cycles).  D = 64 (8 chunks, two rows per bank
+// line): the same properties with 8 rows.
 template <int D>
 __device__ __forceinline__ int swz(int r) {
   if constexpr (D == 128) {
-    return ((r & 7) << 1) | ((r >> 3) & 1);
+    return ((r & 3) << 2) | ((r >> 2) & 3);
   } else {
     return ((r & 3) << 1) | ((r >> 2) & 1);
   }
