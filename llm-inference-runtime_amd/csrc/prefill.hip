@@ -117,13 +117,16 @@ struct PrefillCfg {
 // either read (measured with SQ_LDS_BANK_CONFLICT; the previous
 // ((r & 7) << 1) | ((r >> 3) & 1) left the transpose reads 2-way
 // conflicted, half their LDS cycles).  D = 64 (8 chunks, two rows per bank
-// line): the same properties with 8 rows.
+// line, so a K read's 16 rows share 8 lines): bits 1-2 of r, and r1 ^ r3 on
+// top, is conflict-free for both reads in a model of the bank mapping that
+// reproduces the D = 128 measurements (the previous
+// ((r & 3) << 1) | ((r >> 2) & 1) left the K reads 2-way conflicted there).
 template <int D>
 __device__ __forceinline__ int swz(int r) {
   if constexpr (D == 128) {
     return ((r & 3) << 2) | ((r >> 2) & 3);
   } else {
-    return ((r & 3) << 1) | ((r >> 2) & 1);
+    return ((r >> 1) & 3) | ((((r >> 1) ^ (r >> 3)) & 1) << 2);
   }
 }
 
