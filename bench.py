@@ -255,7 +255,10 @@ def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
         with torch.cuda.graph(g):
             step(t)
         graphs.append(g)
-    graph_ms = _time_ms(lambda i: graphs[i % reps].replay(), steps, warmup)
+    graph1_ms = _time_ms(lambda i: graphs[i % reps].replay(), steps, warmup)
+    # an engine captures a whole forward (every layer's call) in one graph:
+    # `steps` calls in one graph spread the graph launch over them
+    graph_ms = _time_graph_ms(lambda i: step(inst[i % reps]), steps, warmup)
     # metadata of the batch from a block table on the device
     m = w.meta
     npg = np.diff(m.kv_indptr)
@@ -271,6 +274,8 @@ def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
     torch.cuda.empty_cache()
     return {"eager_ms_per_step": eager_ms, "eager_GBps": alg_step / (eager_ms * 1e-3) / 1e9,
             "graph_ms_per_step": graph_ms, "graph_GBps": alg_step / (graph_ms * 1e-3) / 1e9,
+            "graph_steps_per_graph": steps,
+            "graph_one_step_ms": graph1_ms,
             "metadata_build_ms": meta_ms}
 
 
@@ -499,7 +504,9 @@ def main() -> int:
         }
         dp = bench_device_plan(main_w, dev, dtype)
         log(f"tinyllama_decode (device plan): eager {dp['eager_ms_per_step']:.4f} ms, "
-            f"HIP graph replay {dp['graph_ms_per_step']:.4f} ms; metadata build "
+            f"HIP graph {dp['graph_ms_per_step']:.4f} ms per step "
+            f"({dp['graph_steps_per_graph']} steps per graph; "
+            f"{dp['graph_one_step_ms']:.4f} ms with one step per graph); metadata build "
             f"{1e3 * dp['metadata_build_ms']:.1f} us")
         extra["tinyllama_decode.device_plan"] = dp
         kw = bench_kv_write(dev)
