@@ -112,10 +112,15 @@ int pagedattn_apply_rope_pos_ids_inplace(
  * Bit-exact copy when cache_dtype == src_dtype.  cache_dtype E4M3 stores
  * round_to_nearest_even(clamp(x / scale, -448, 448)) with scale =
  * kv_scales[(page*2 + {0,1})*num_kv_heads + h] (kv_scales may be NULL
- * otherwise).  kv_last_page_len is accepted for interface parity and, as in
- * the reference kernel, not used for addressing (may be NULL).
- * Tokens whose batch index, page slot or page id fall outside the metadata
- * are skipped and counted in *error_flag (int32, device; may be NULL). */
+ * otherwise); a block whose scale is not positive and finite gets zero
+ * codes.  kv_last_page_len is accepted for interface parity and, as in the
+ * reference kernel, not used for addressing (may be NULL).
+ * *error_flag (int32, device; may be NULL) is incremented once per token
+ * whose batch index, page slot or page id fall outside the metadata (the
+ * token is skipped) and, for E4M3, once per 8-element piece of a written
+ * row (elements [8i, 8i+8) of one K or V head row) in which some
+ * |x / scale| exceeded 448 or whose scale was not positive and finite.
+ * Zero after a call means every token landed unclamped. */
 int pagedattn_append_paged_kv_cache(
     const void* append_key, const void* append_value, int64_t k_stride_n,
     int64_t k_stride_h, int64_t v_stride_n, int64_t v_stride_h,
@@ -133,8 +138,8 @@ int pagedattn_append_paged_kv_cache(
  * full head (non-interleaved halves) exactly as
  * pagedattn_apply_rope_pos_ids_inplace does, and the rotated K rows and the
  * V rows are written to their page slots as pagedattn_append_paged_kv_cache
- * does.  head_dim must be a multiple of 16.  Same metadata, error and e4m3
- * contract as pagedattn_append_paged_kv_cache. */
+ * does.  head_dim must be a multiple of 16.  Same metadata, error_flag and
+ * e4m3 contract as pagedattn_append_paged_kv_cache. */
 int pagedattn_rope_append_paged_kv_cache(
     void* q, int64_t q_stride_n, int64_t q_stride_h, int32_t num_qo_heads,
     void* append_key, const void* append_value, int64_t k_stride_n,
@@ -229,7 +234,10 @@ int pagedattn_build_paged_metadata(const int32_t* block_tables, int64_t table_st
  * chunks of that many pages (rounded up to a multiple of 8); 0 lets the
  * planner choose from the device's CU count; -1 disables splitting.
  * The work list and split partials are placed in `workspace` (device,
- * workspace_bytes long) with one hipMemcpyAsync on `stream`. */
+ * 256-byte aligned, workspace_bytes long) from byte 256 on, with one
+ * hipMemcpyAsync on `stream`.  Bytes [0, 256) are the caller's, except the
+ * int32 at byte 0: the error counter that the fused-append decode runs
+ * increment (never cleared by the library). */
 pagedattn_plan* pagedattn_plan_create(void);
 void pagedattn_plan_destroy(pagedattn_plan* plan);
 
@@ -281,6 +289,13 @@ int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
  * [B, num_kv_heads, head_dim] (q dtype, strided) are written into slot
  * kv_len_b - 1 of each sequence's last page (e4m3 pools: round(clamp(x /
  * scale, +-448)) with that page's scale) and take part in the attention.
+ * Row b must be sequence b's new token: the caller's batch_indices of the
+ * step must be arange(B) (src/engine/runtime/step_executor.py:220-222);
+ * other token orders go through pagedattn_append_paged_kv_cache and
+ * pagedattn_decode_run.  A sequence (with pages) whose new token falls
+ * outside its pages or on an invalid page id is not appended, and e4m3
+ * pieces clamped as in pagedattn_append_paged_kv_cache are counted, in the
+ * int32 at byte 0 of the plan's workspace.
  * Same plan, pool and output contract as pagedattn_decode_run. */
 int pagedattn_decode_run_append(
     const pagedattn_plan* plan, const void* q, int64_t q_stride_n,
@@ -302,7 +317,8 @@ int pagedattn_decode_run_append(
  * RoPE angle, and page positions/16, slot positions%16 of the append (a
  * position outside the sequence's pages is skipped).  Rotation math is the
  * one of pagedattn_apply_rope_pos_ids_inplace, so the output and the pool
- * equal (bit for bit) those of the three separate calls. */
+ * equal (bit for bit) those of the three separate calls.  Same row order
+ * requirement and error counter as pagedattn_decode_run_append. */
 int pagedattn_decode_run_rope_append(
     const pagedattn_plan* plan, const void* q, int64_t q_stride_n,
     int64_t q_stride_h, int32_t q_dtype, const void* append_key,

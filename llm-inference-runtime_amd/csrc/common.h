@@ -129,6 +129,46 @@ __device__ __forceinline__ uint32_t f32_to_e4m3x4(float a, float b, float c,
   return (uint32_t)w;
 }
 
+// Eight 16-bit values (u32x4) -> eight e4m3 bytes with a fixed scale:
+// round_to_nearest_even(clamp(x / scale, -448, 448)).  *clamped is set when
+// a value had |x / scale| > 448 (or x / scale was NaN) and the clamp changed
+// it.  A scale that is not positive and finite writes zero codes and sets
+// *clamped.  Every kernel that appends with a fixed scale uses this one, so
+// the stand-alone, RoPE-fused and decode-fused appends store the same bytes.
+template <bool IS_BF16>
+__device__ __forceinline__ u32x2 quant8_e4m3(u32x4 x, float scale, bool* clamped) {
+  float f[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[2 * e] = h2f<IS_BF16>((uint16_t)(x[e] & 0xffffu));
+    f[2 * e + 1] = h2f<IS_BF16>((uint16_t)(x[e] >> 16));
+  }
+  bool over = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float y = f[e] / scale;
+    over |= !(__builtin_fabsf(y) <= 448.f);
+    f[e] = fminf(fmaxf(y, -448.f), 448.f);
+  }
+  u32x2 o;
+  o[0] = f32_to_e4m3x4(f[0], f[1], f[2], f[3]);
+  o[1] = f32_to_e4m3x4(f[4], f[5], f[6], f[7]);
+  const bool scale_ok = scale > 0.f && scale < __builtin_huge_valf();
+  if (!scale_ok) o = u32x2{0u, 0u};
+  *clamped = over || !scale_ok;
+  return o;
+}
+
+// Adds the number of active lanes with `hit` set to *counter (a device int32;
+// may be null) with one atomic per wave, issued by the first such lane.
+// Lanes that call it from different branches are counted by their own call.
+__device__ __forceinline__ void count_lanes(int32_t* counter, bool hit) {
+  const uint64_t m = __builtin_amdgcn_ballot_w64(hit);
+  if (m == 0 || counter == nullptr) return;
+  const int lane = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  if (lane == __builtin_ctzll(m)) atomicAdd(counter, (int32_t)__builtin_popcountll(m));
+}
+
 // RoPE (src/models/llama.py:175-182 via flashinfer.apply_rope_pos_ids_inplace):
 // angle of frequency i at position pos, inv_freq = theta^(-2i/rotary_dim),
 // pos / rope_scale, formed and reduced mod 2 pi in fp64 so that positions up

@@ -37,6 +37,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <queue>
 #include <vector>
 
@@ -75,6 +76,9 @@ struct DecodeParams {
   // new_pos % 16, and the fused RoPE rotates q and the new K row there
   const int32_t* new_pos;
   double rope_inv_scale, rope_log2_theta;
+  // fused append: tokens skipped (position outside the sequence's pages or
+  // an invalid page id) and clamped e4m3 chunks are counted here (may be null)
+  int32_t* append_err;
 };
 
 #ifndef DECODE_KV_POLICY
@@ -457,22 +461,6 @@ __device__ __forceinline__ void compute_pairs(const Stage<D, BF16, FP8> (&st)[NP
   }
 }
 
-// 8 sixteen-bit values -> 8 e4m3 bytes, round(clamp(x / scale, +-448)).
-template <bool BF16>
-__device__ __forceinline__ u32x2 quant8(u32x4 x, float scale) {
-  float f[8];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    f[2 * e] = h2f<BF16>((uint16_t)(x[e] & 0xffffu));
-    f[2 * e + 1] = h2f<BF16>((uint16_t)(x[e] >> 16));
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / scale, -448.f), 448.f);
-  u32x2 o;
-  o[0] = f32_to_e4m3x4(f[0], f[1], f[2], f[3]);
-  o[1] = f32_to_e4m3x4(f[4], f[5], f[6], f[7]);
-  return o;
-}
 // Writes sequence b / head h's new row to slot `slot` of page `page` (the
 // append of flashinfer.append_paged_kv_cache at position kv_len - 1) and to
 // the wave's LDS slot `new_row`.  Lanes [0, D/8) move the K row, lanes
@@ -491,9 +479,11 @@ __device__ __forceinline__ void put_chunk(const DecodeParams& p, uint8_t* new_ro
   if constexpr (FP8) {
     const float scale =
         load_invariant(p.kv_scales + ((int64_t)page * 2 + is_v) * p.hkv + h);
-    const u32x2 q = quant8<BF16>(x, scale);
+    bool clamped = false;
+    const u32x2 q = quant8_e4m3<BF16>(x, scale, &clamped);
     *reinterpret_cast<u32x2*>(dst) = q;
     *reinterpret_cast<u32x2*>(lds) = q;
+    count_lanes(p.append_err, clamped);
   } else {
     *reinterpret_cast<u32x4*>(dst) = x;
     *reinterpret_cast<u32x4*>(lds) = x;
@@ -599,14 +589,23 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
     const int new_slot = new_pos & (kPage - 1);
     if constexpr (APPEND) {
       const int pg = new_pos >= 0 ? new_pos / kPage : -1;
-      if (pg >= 0 && pg < npages && pg >= page_lo && pg < page_hi) {
-        const int page = page_id(p, ind_lo, pg, npages);
-        if (page >= 0) {
-          new_pg = pg;
-          fused_append<D, BF16, FP8, ROPE>(p, new_row, b, h, page, new_slot, lane,
-                                           new_pos);
+      bool skipped = false;
+      if (pg >= 0 && pg < npages) {
+        if (pg >= page_lo && pg < page_hi) {
+          const int page = page_id(p, ind_lo, pg, npages);
+          if (page >= 0) {
+            new_pg = pg;
+            fused_append<D, BF16, FP8, ROPE>(p, new_row, b, h, page, new_slot, lane,
+                                             new_pos);
+          } else {
+            skipped = true;
+          }
         }
+      } else {
+        // outside the sequence's pages: counted by its first piece
+        skipped = npages > 0 && page_lo == 0;
       }
+      count_lanes(p.append_err, skipped && h == 0 && lane == 0);
     }
 
     SoftmaxState<D, BF16, FP8> sm;
@@ -949,6 +948,50 @@ static int decode_head_group(int hkv) {
   return hg;
 }
 
+// The device-side partition of a decode plan (pagedattn_decode_plan_device
+// and pagedattn_decode_run_noalloc): shares of the (sequence, head group,
+// page) stream for cus x waves-per-CU / hg head groups, split partials at
+// `partials` (256-byte aligned, `bytes` long).
+static int setup_device_plan(const char* who, pagedattn_plan* plan, int32_t batch_size,
+                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t page_size, int cus, char* partials, size_t bytes) {
+  plan->mode = kPlanNone;
+  if (batch_size < 0)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: batch_size %d < 0", who, batch_size);
+  int rc = validate_heads(who, num_qo_heads, num_kv_heads, head_dim, page_size);
+  if (rc) return rc;
+  const int hg = decode_head_group(num_kv_heads);
+  const int g = num_qo_heads / num_kv_heads;
+  const int n_groups = std::max(1, cus * decode_waves_per_cu() / hg);
+  const int n_slots = 2 * n_groups * hg;
+  const size_t off_pl = ws_align(sizeof(float) * (size_t)n_slots * g * head_dim);
+  const size_t end = ws_align(off_pl + sizeof(float) * (size_t)n_slots * g);
+  if (end > bytes)
+    return set_error(PAGEDATTN_ERR_WORKSPACE, "%s: needs %zu bytes of split partials, %zu "
+                     "available", who, end, bytes);
+  plan->implicit = true;
+  plan->item_cost = decode_item_cost();
+  plan->batch_size = batch_size;
+  plan->hq = num_qo_heads;
+  plan->hkv = num_kv_heads;
+  plan->d = head_dim;
+  plan->page_size = page_size;
+  plan->n_items = n_groups;
+  plan->hg_shift = hg == 4 ? 2 : hg == 2 ? 1 : 0;
+  plan->n_merge = 0;
+  plan->n_slots = n_slots;
+  plan->split_pages = 0;
+  plan->items_dev = nullptr;
+  plan->wave_ptr_dev = nullptr;
+  plan->merge_dev = nullptr;
+  plan->partial_o = reinterpret_cast<float*>(partials);
+  plan->partial_lse = reinterpret_cast<float*>(partials + off_pl);
+  plan->total_pages = -1;
+  plan->max_pages = -1;
+  plan->mode = kPlanDecode;
+  return PAGEDATTN_OK;
+}
+
 }  // namespace pa
 
 using namespace pa;
@@ -1173,49 +1216,21 @@ int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
   const char* who = "decode_plan_device";
   if (!plan) return set_error(PAGEDATTN_ERR_INVALID, "%s: null plan", who);
   plan->mode = kPlanNone;
-  if (batch_size < 0)
-    return set_error(PAGEDATTN_ERR_INVALID, "%s: batch_size %d < 0", who, batch_size);
-  int rc = validate_heads(who, num_qo_heads, num_kv_heads, head_dim, page_size);
-  if (rc) return rc;
   if (!workspace || ((uintptr_t)workspace & (kWsAlign - 1)))
     return set_error(PAGEDATTN_ERR_INVALID,
                      "%s: workspace must be a 256-byte aligned device buffer", who);
   int cus = device_cu_count();
   if (cus <= 0) cus = 256;
-  const int hg = decode_head_group(num_kv_heads);
-  const int g = num_qo_heads / num_kv_heads;
-  const int n_groups = std::max(1, cus * decode_waves_per_cu() / hg);
-  const int n_slots = 2 * n_groups * hg;
-  const size_t off_po = ws_align(kWsHeader);
-  const size_t off_pl = ws_align(off_po + sizeof(float) * (size_t)n_slots * g * head_dim);
-  const size_t end = ws_align(off_pl + sizeof(float) * (size_t)n_slots * g);
-  if (end > workspace_bytes)
-    return set_error(PAGEDATTN_ERR_WORKSPACE, "%s: needs %zu workspace bytes, %zu available",
-                     who, end, workspace_bytes);
-  char* ws = static_cast<char*>(workspace);
+  if (workspace_bytes < kWsHeader)
+    return set_error(PAGEDATTN_ERR_WORKSPACE, "%s: workspace smaller than its %zu-byte header",
+                     who, kWsHeader);
   plan->host.clear();
+  const int rc = setup_device_plan(who, plan, batch_size, num_qo_heads, num_kv_heads, head_dim,
+                                   page_size, cus, static_cast<char*>(workspace) + kWsHeader,
+                                   workspace_bytes - kWsHeader);
+  if (rc) return rc;
   plan->workspace = workspace;
   plan->workspace_bytes = workspace_bytes;
-  plan->implicit = true;
-  plan->item_cost = decode_item_cost();
-  plan->batch_size = batch_size;
-  plan->hq = num_qo_heads;
-  plan->hkv = num_kv_heads;
-  plan->d = head_dim;
-  plan->page_size = page_size;
-  plan->n_items = n_groups;
-  plan->hg_shift = hg == 4 ? 2 : hg == 2 ? 1 : 0;
-  plan->n_merge = 0;
-  plan->n_slots = n_slots;
-  plan->split_pages = 0;
-  plan->items_dev = nullptr;
-  plan->wave_ptr_dev = nullptr;
-  plan->merge_dev = nullptr;
-  plan->partial_o = reinterpret_cast<float*>(ws + off_po);
-  plan->partial_lse = reinterpret_cast<float*>(ws + off_pl);
-  plan->total_pages = -1;
-  plan->max_pages = -1;
-  plan->mode = kPlanDecode;
   return PAGEDATTN_OK;
 }
 
@@ -1231,6 +1246,9 @@ struct AppendRows {
   bool rope;
   const int32_t* new_pos;
   double rope_inv_scale, rope_log2_theta;
+  // fused append: tokens skipped (position outside the sequence's pages or
+  // an invalid page id) and clamped e4m3 chunks are counted here (may be null)
+  int32_t* append_err;
 };
 
 static int decode_run_impl(const char* who, const pagedattn_plan* plan,
@@ -1306,6 +1324,7 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   p.new_pos = app ? app->new_pos : nullptr;
   p.rope_inv_scale = app ? app->rope_inv_scale : 1.0;
   p.rope_log2_theta = app ? app->rope_log2_theta : 0.0;
+  p.append_err = app ? app->append_err : nullptr;
 
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = q_dtype == PAGEDATTN_BF16;
@@ -1376,8 +1395,10 @@ int pagedattn_decode_run_append(
                      "%s: append rows must be 16-byte aligned with strides that "
                      "are multiples of 8 elements",
                      who);
+  // skips and clamps are counted in the int32 at byte 0 of the workspace
   AppendRows app{append_key, append_value, k_stride_n, k_stride_h,
-                 v_stride_n, v_stride_h, q_dtype, false, nullptr, 1.0, 0.0};
+                 v_stride_n, v_stride_h, q_dtype, false, nullptr, 1.0, 0.0,
+                 plan ? static_cast<int32_t*>(plan->workspace) : nullptr};
   return decode_run_impl(who, plan, q, q_stride_n, q_stride_h, q_dtype,
                          paged_kv_cache, kv_dtype, kv_scales, num_pages,
                          kv_indices, num_indices, kv_indptr, kv_last_page_len,
@@ -1408,7 +1429,8 @@ int pagedattn_decode_run_rope_append(
                      who);
   AppendRows app{append_key, append_value, k_stride_n, k_stride_h, v_stride_n,
                  v_stride_h, q_dtype, true, positions, 1.0 / (double)rope_scale,
-                 std::log2((double)rope_theta)};
+                 std::log2((double)rope_theta),
+                 plan ? static_cast<int32_t*>(plan->workspace) : nullptr};
   return decode_run_impl(who, plan, q, q_stride_n, q_stride_h, q_dtype,
                          paged_kv_cache, kv_dtype, kv_scales, num_pages,
                          kv_indices, num_indices, kv_indptr, kv_last_page_len,

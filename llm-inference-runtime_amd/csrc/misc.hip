@@ -63,10 +63,30 @@ __global__ void __launch_bounds__(256)
 }
 
 // ----------------------------------------------------------------------------
+// Writes one 8-element chunk of a K (kind 0) or V (kind 1) row of head h to
+// slot `slot` of `page`.  e4m3 pools: quantised with the page's fixed scale
+// (quant8_e4m3); a clamped chunk is counted in *a.err.
+template <bool IS_BF16, bool TO_FP8>
+__device__ __forceinline__ void store_chunk(const AppendArgs& a, int64_t page, int slot,
+                                            int kind, int h, int d0, u32x4 x) {
+  const int64_t dst_elem =
+      (((page * 2 + kind) * a.hkv + h) * kPage + slot) * (int64_t)a.d + d0;
+  if constexpr (!TO_FP8) {
+    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.cache) + dst_elem) = x;
+  } else {
+    const float scale = a.scales[(page * 2 + kind) * a.hkv + h];
+    bool clamped = false;
+    const u32x2 o = quant8_e4m3<IS_BF16>(x, scale, &clamped);
+    *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(a.cache) + dst_elem) = o;
+    count_lanes(a.err, clamped);
+  }
+}
+
 // append_paged_kv_cache (src/models/llama.py:188-210), HND pool.  One thread
 // moves one 16-byte chunk (8 elements) of one head of K or V, so a wave
 // writes whole 128/256-byte page rows.  Metadata outside its ranges skips the
-// token and bumps *err instead of faulting.
+// token and bumps *err instead of faulting (once per token); e4m3 chunks
+// whose values were clamped bump it once per chunk.
 template <bool FP8_IS_BF16_SRC, bool TO_FP8>
 __global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
   const int chunks = a.d >> 3;  // 8 elements per chunk
@@ -80,57 +100,13 @@ __global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
   int slot = 0;
   const int64_t page = append_target_page(a, j, &slot);
   if (page < 0) {
-    if (c == 0 && h == 0 && kind == 0 && a.err) atomicAdd(a.err, 1);
+    count_lanes(a.err, c == 0 && h == 0 && kind == 0);
     return;
   }
   const uint16_t* src = kind ? a.v + (int64_t)j * a.v_sn + (int64_t)h * a.v_sh
                              : a.k + (int64_t)j * a.k_sn + (int64_t)h * a.k_sh;
-  const int64_t dst_elem =
-      (((page * 2 + kind) * a.hkv + h) * kPage + slot) * (int64_t)a.d + c * 8;
-  const u32x4 x = *reinterpret_cast<const u32x4*>(src + c * 8);
-  if constexpr (!TO_FP8) {
-    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.cache) + dst_elem) = x;
-  } else {
-    const float scale = a.scales[(page * 2 + kind) * a.hkv + h];
-    float f[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      f[2 * e] = h2f<FP8_IS_BF16_SRC>((uint16_t)(x[e] & 0xffffu));
-      f[2 * e + 1] = h2f<FP8_IS_BF16_SRC>((uint16_t)(x[e] >> 16));
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / scale, -448.f), 448.f);
-    u32x2 o;
-    o[0] = f32_to_e4m3x4(f[0], f[1], f[2], f[3]);
-    o[1] = f32_to_e4m3x4(f[4], f[5], f[6], f[7]);
-    *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(a.cache) + dst_elem) = o;
-  }
-}
-
-// Writes one 8-element chunk of a K (kind 0) or V (kind 1) row of head h to
-// slot `slot` of `page` (e4m3 pools: quantised with the page's scale).
-template <bool IS_BF16, bool TO_FP8>
-__device__ __forceinline__ void store_chunk(const AppendArgs& a, int64_t page, int slot,
-                                            int kind, int h, int d0, u32x4 x) {
-  const int64_t dst_elem =
-      (((page * 2 + kind) * a.hkv + h) * kPage + slot) * (int64_t)a.d + d0;
-  if constexpr (!TO_FP8) {
-    *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(a.cache) + dst_elem) = x;
-  } else {
-    const float scale = a.scales[(page * 2 + kind) * a.hkv + h];
-    float f[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      f[2 * e] = h2f<IS_BF16>((uint16_t)(x[e] & 0xffffu));
-      f[2 * e + 1] = h2f<IS_BF16>((uint16_t)(x[e] >> 16));
-    }
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = fminf(fmaxf(f[e] / scale, -448.f), 448.f);
-    u32x2 o;
-    o[0] = f32_to_e4m3x4(f[0], f[1], f[2], f[3]);
-    o[1] = f32_to_e4m3x4(f[4], f[5], f[6], f[7]);
-    *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(a.cache) + dst_elem) = o;
-  }
+  store_chunk<FP8_IS_BF16_SRC, TO_FP8>(a, page, slot, kind, h, c * 8,
+                                       *reinterpret_cast<const u32x4*>(src + c * 8));
 }
 
 // ----------------------------------------------------------------------------
@@ -173,7 +149,7 @@ __global__ void __launch_bounds__(256) rope_append_kernel(RopeAppendArgs r) {
     }
     int slot = 0;
     const int64_t page = append_target_page(a, j, &slot);
-    if (page < 0 && c == 0 && a.err) atomicAdd(a.err, 1);
+    count_lanes(a.err, page < 0 && c == 0);
     for (int h = 0; h < a.hkv; ++h) {
       uint16_t* x = const_cast<uint16_t*>(a.k) + (int64_t)j * a.k_sn + (int64_t)h * a.k_sh;
       u32x4 lo = *reinterpret_cast<const u32x4*>(x + 8 * c);

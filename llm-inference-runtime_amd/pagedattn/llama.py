@@ -64,6 +64,11 @@ class FlashInferState:
 
     mode: str = "prefill"
 
+    # set by plan_decode: (batch_indices tensor, its version) when the step's
+    # token rows are sequences 0..B-1 in order, which the fused decode launch
+    # requires; None otherwise
+    _fused_rows: tuple | None = None
+
 
 WORKSPACE_BYTES = 128 * 1024 * 1024
 
@@ -89,8 +94,11 @@ def init_flashinfer_state(*, kv_pool: torch.Tensor, page_size: int, device,
 
 
 def append_error_count() -> int:
-    """Tokens the page append skipped because their metadata pointed outside
-    the page table since init (reads the device counter: synchronises)."""
+    """The page appends' error counter since init (reads the device counter:
+    synchronises): tokens skipped because their metadata pointed outside the
+    page table, plus, for e4m3 pools with fixed scales, 8-element pieces of
+    written rows that were clamped at +-448 (or met a bad scale).  The fused
+    decode launches count into the same int32 (byte 0 of the workspace)."""
     ws = FlashInferState.workspace_buffer
     if ws is None:
         return 0
@@ -134,6 +142,20 @@ def plan_decode(*, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
     dw = cast(ops.BatchDecodeWithPagedKVCacheWrapper, FlashInferState.decode_wrapper)
     dw.begin_forward(kv_indptr, kv_indices, kv_last_page_len, num_qo_heads, num_kv_heads,
                      head_dim, FlashInferState.page_size, q_data_type=_q_dtype())
+    FlashInferState._fused_rows = _identity_rows(FlashInferState.batch_indices,
+                                                 kv_last_page_len.numel())
+
+
+def _identity_rows(batch_indices: torch.Tensor | None, bsz: int) -> tuple | None:
+    """(batch_indices, its in-place version) when it is arange(bsz), the
+    engine's decode rows (step_executor.py:220-222), else None.  Reads the
+    tensor on the host: the plan already waits for its metadata copy."""
+    if batch_indices is None or batch_indices.numel() != bsz:
+        return None
+    got = batch_indices.detach().to("cpu", torch.int64)
+    if not torch.equal(got, torch.arange(bsz, dtype=torch.int64)):
+        return None
+    return batch_indices, batch_indices._version
 
 
 def patched_llama_attention_forward(self, hidden_states: torch.Tensor,
@@ -209,12 +231,17 @@ def patched_llama_attention_forward(self, hidden_states: torch.Tensor,
 
 
 def _decode_rows_match(q_rows: torch.Tensor) -> bool:
-    """The fused decode launch appends row b at kv_len_b - 1: it applies when
-    the step carries exactly one new token per planned sequence, laid out in
-    sequence order (batch_indices = arange(B)), as the engine's decode step
-    does (step_executor.py:204-234)."""
+    """The fused decode launch appends row b to sequence b: it applies when
+    the step carries exactly one new token per planned sequence in sequence
+    order, i.e. the batch_indices that plan_decode saw were arange(B) and
+    that tensor is still the state's, unmodified (the engine's decode step,
+    step_executor.py:204-234).  Otherwise the separate RoPE + append and
+    attention launches run, which honour any batch_indices."""
     dw = cast(ops.BatchDecodeWithPagedKVCacheWrapper, FlashInferState.decode_wrapper)
-    return q_rows.shape[0] == getattr(dw, "_bsz", -1)
+    rec = FlashInferState._fused_rows
+    bi = FlashInferState.batch_indices
+    return (rec is not None and rec[0] is bi and bi._version == rec[1]
+            and q_rows.shape[0] == getattr(dw, "_bsz", -1))
 
 
 def _fuse_qkv_proj(attn) -> nn.Linear:

@@ -164,9 +164,12 @@ def append_paged_kv_cache(append_key: torch.Tensor, append_value: torch.Tensor,
     """Scatter k/v rows into their pages (src/models/llama.py:188-210).
 
     Bit-exact for a pool of the source dtype; an e4m3 pool stores
-    round(clamp(x / scale, +-448)) with kv_scales [num_pages, 2, Hkv].
-    `error_flag` (int32 device scalar, optional) counts tokens whose metadata
-    pointed outside the page table; those tokens are skipped."""
+    round(clamp(x / scale, +-448)) with kv_scales [num_pages, 2, Hkv] (zero
+    codes where a scale is not positive and finite).
+    `error_flag` (int32 device scalar, optional) is incremented once per
+    token whose metadata pointed outside the page table (the token is
+    skipped) and, for e4m3, once per 8-element piece of a written row that
+    was clamped or had a bad scale; zero means every token landed intact."""
     num_pages, hkv, d = _check_pool(paged_kv_cache, None, None, kv_layout)
     _check_rows(append_key, "append_key", hkv, d)
     _check_rows(append_value, "append_value", hkv, d)
@@ -739,36 +742,6 @@ class BatchPrefillWithPagedKVCacheWrapper(_WrapperBase):
         self._bsz, self._hq, self._hkv, self._d = (bsz, int(num_qo_heads), int(num_kv_heads),
                                                    int(head_dim_qk))
         self._causal = bool(causal)
-        self._sm_scale = sm_scale
-        self._planned = True
-
-    def _plan_device(self, indptr, indices, last_page_len, num_qo_heads, num_kv_heads,
-                     head_dim, page_size, q_data_type, kv_data_type, data_type, sm_scale):
-        device = self._ws.device
-        bsz = last_page_len.numel()
-        if indptr.numel() != bsz + 1:
-            raise ValueError(f"indptr has {indptr.numel()} entries for {bsz} sequences")
-        if self._graph_bufs is not None:
-            b_indptr, b_indices, b_last = self._graph_bufs
-            if b_last.numel() != bsz:
-                raise ValueError(f"the graph buffers hold {b_last.numel()} sequences, "
-                                 f"the plan has {bsz}")
-            if indices.numel() > b_indices.numel():
-                raise ValueError("indices do not fit paged_kv_indices_buffer")
-            for src, dst in ((indptr, b_indptr), (last_page_len, b_last),
-                             (indices, b_indices[:indices.numel()])):
-                if src.data_ptr() != dst.data_ptr():
-                    dst.copy_(src, non_blocking=True)
-            self._indptr, self._indices, self._last = b_indptr, b_indices, b_last
-        else:
-            self._indptr = _i32(indptr, device)
-            self._indices = _i32(indices, device)
-            self._last = _i32(last_page_len, device)
-        self._q_dtype = _dtype_of(data_type if data_type is not None else q_data_type)
-        self._kv_dtype = _dtype_of(kv_data_type) if kv_data_type is not None else None
-        call("pagedattn_decode_plan_device", self._plan.handle, bsz, int(num_qo_heads),
-             int(num_kv_heads), int(head_dim), int(page_size), ptr(self._ws), self._ws_bytes)
-        self._bsz, self._hq, self._hkv, self._d = bsz, int(num_qo_heads), int(num_kv_heads), int(head_dim)
         self._sm_scale = sm_scale
         self._planned = True
 

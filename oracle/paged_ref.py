@@ -19,7 +19,8 @@ E4M3_MAX = 448.0
 
 __all__ = [
     "PAGE", "E4M3_MAX", "kv_lengths", "batch_indices_positions", "append_pages",
-    "e4m3_encode", "e4m3_decode", "quantize_pages", "append_pages_e4m3", "pow2_scale",
+    "e4m3_encode", "e4m3_decode", "quantize_pages", "append_pages_e4m3",
+    "e4m3_clamped_pieces", "pow2_scale",
     "append_pages_e4m3_running", "fork_pages", "gather_pages",
     "attention", "decode", "prefill", "split_attention", "merge_states", "rope",
     "to_bits", "from_bits",
@@ -150,21 +151,64 @@ def quantize_pages(pool: torch.Tensor):
     return bits, scale
 
 
+def _scale_ok(scale: torch.Tensor) -> torch.Tensor:
+    return (scale > 0) & torch.isfinite(scale)
+
+
+def _encode_fixed(x: torch.Tensor, scale: torch.Tensor) -> np.ndarray:
+    """e4m3_encode of rows x [n, H, D] with per-(row, head) scales [n, H, 1];
+    rows whose scale is not positive and finite become zero codes."""
+    bits = e4m3_encode(x, scale)
+    bad = (~_scale_ok(scale)).expand_as(x).numpy()
+    bits[bad] = 0
+    return bits
+
+
 def append_pages_e4m3(pool_bits: np.ndarray, scales: torch.Tensor, k: torch.Tensor,
                       v: torch.Tensor, batch_indices, positions, kv_indices, kv_indptr):
-    """append_pages into an e4m3 pool: rows are encoded with the scale of
-    their target (page, K|V, head).  Returns (new_pool_bits, skipped)."""
+    """append_pages (the scatter of src/models/llama.py:188-210 onto the
+    allocator.py:25-36 layout) into an e4m3 pool with fixed scales: row
+    (token j, K|V, head h) landing in page p is stored as
+    e4m3(round(clamp(x / scales[p, K|V, h], +-448))), or as zero codes when
+    that scale is not positive and finite.  Returns (new_pool_bits, skipped).
+    Pinned by: test_append_e4m3_loop (pure-Python per-element loop with a
+    brute-force e4m3 rounding) and test_e4m3_pins_catch_planted_mistakes."""
     out = pool_bits.copy()
     ok, page_id, slot = _append_targets(batch_indices, positions, kv_indices, kv_indptr,
                                         pool_bits.shape[0])
     js = np.nonzero(ok)[0]
     if len(js):
         pj = torch.from_numpy(page_id[js])
-        ks = scales[pj, 0][:, :, None]  # [n, H, 1]
-        vs = scales[pj, 1][:, :, None]
-        out[page_id[js], 0, :, slot[js], :] = e4m3_encode(k[js].float(), ks)
-        out[page_id[js], 1, :, slot[js], :] = e4m3_encode(v[js].float(), vs)
+        ks = scales[pj, 0][:, :, None].float()  # [n, H, 1]
+        vs = scales[pj, 1][:, :, None].float()
+        out[page_id[js], 0, :, slot[js], :] = _encode_fixed(k[js].float(), ks)
+        out[page_id[js], 1, :, slot[js], :] = _encode_fixed(v[js].float(), vs)
     return out, int((~ok).sum())
+
+
+def e4m3_clamped_pieces(k: torch.Tensor, v: torch.Tensor, scales: torch.Tensor,
+                        batch_indices, positions, kv_indices, kv_indptr,
+                        num_pages: int) -> int:
+    """What a fixed-scale e4m3 append counts besides skipped tokens: over the
+    rows it writes (token, K|V, head), the 8-element pieces [8i, 8i + 8) in
+    which some |x / scale| > 448 (the clamp changes a value) or whose scale is
+    not positive and finite.
+    Pinned by: test_e4m3_clamped_pieces_loop (pure-Python loop)."""
+    ok, page_id, _ = _append_targets(batch_indices, positions, kv_indices, kv_indptr,
+                                     num_pages)
+    js = np.nonzero(ok)[0]
+    if not len(js):
+        return 0
+    pj = torch.from_numpy(page_id[js])
+    n = 0
+    for kind, src in ((0, k), (1, v)):
+        x = src[js].float()  # [n, H, D]
+        s = scales[pj, kind][:, :, None].float()
+        over = ~((x / s).abs() <= E4M3_MAX)  # NaN counts as over
+        over = over | ~_scale_ok(s)
+        d = x.shape[-1]
+        n += int(over.reshape(x.shape[0], x.shape[1], d // 8, 8).any(-1).sum())
+    return n
 
 
 def pow2_scale(amax) -> np.ndarray:
@@ -274,8 +318,10 @@ def gather_pages(pool: torch.Tensor, kv_indptr, kv_indices, last_page_len, b: in
     """Dense K, V [kv_len, H, D] of sequence b from the HND pool
     (allocator.py:25-36 layout; kv_indices[kv_indptr[b]:kv_indptr[b+1]] is the
     block table, step_executor.py:137-144).  e4m3 pools are dequantised with
-    their per-(page, K|V, head) scales.  Pinned by: test_append_gather_roundtrip
-    and test_gather_permutation (permuting physical pages permutes nothing)."""
+    their per-(page, K|V, head) scales: code_value(bits) * scales[page, K|V, h].
+    Pinned by: test_append_gather_roundtrip, test_gather_permutation (permuting
+    physical pages permutes nothing), test_gather_e4m3_loop (pure-Python
+    per-element decode loop) and test_e4m3_pins_catch_planted_mistakes."""
     indptr = np.asarray(kv_indptr, dtype=np.int64)
     ind = np.asarray(kv_indices, dtype=np.int64)
     pages = ind[indptr[b]:indptr[b + 1]]

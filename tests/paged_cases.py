@@ -104,6 +104,65 @@ def max_err(out, ref, rows=None):
     return float((o - ref).abs().max()) if o.numel() else 0.0
 
 
+def rel_err(out, ref, rows=None):
+    """Largest error of a (row, head) output relative to that row's largest
+    reference value: max|out - ref| / max|ref|.  Attention outputs shrink
+    like sqrt(1 / kv_len) for N(0, 1) data, so an absolute bound alone would
+    accept a near-zero output at long contexts; this one does not."""
+    o = out.float().cpu()
+    r = ref
+    if rows is not None:
+        o, r = o[rows], r[rows]
+    if not o.numel():
+        return 0.0
+    num = (o - r).abs().amax(-1)
+    den = r.abs().amax(-1)
+    keep = torch.isfinite(den) & (den > 0)
+    if not bool(keep.any()):
+        return 0.0
+    return float((num[keep] / den[keep]).max())
+
+
+def scale_keys_by_page(pool, meta, per_page, seqs=None):
+    """Multiplies the K rows of page i of every sequence (i counted within the
+    sequence's table) by 1 + per_page * i: scores then grow from page to
+    page, so the kernels' online softmax must move its running max (and
+    rescale O and l) many times within a sequence, and split pieces carry
+    different maxima into the merge."""
+    factor = torch.ones(pool.shape[0], dtype=torch.float32)
+    for b in (range(len(meta.kv_last_page_len)) if seqs is None else seqs):
+        pages = meta.kv_indices[meta.kv_indptr[b]:meta.kv_indptr[b + 1]]
+        for i, pg in enumerate(pages.tolist()):
+            factor[pg] = 1.0 + per_page * i
+    f = factor.to(pool.device)[:, None, None, None]
+    pool[:, 0] = (pool[:, 0].float() * f).to(pool.dtype)
+    return pool
+
+
+def log2_max_jumps(meta, pool, q, b, slack=8.0, scales=None, sm_scale=None):
+    """How often, over sequence b's pages in order, the running max of the
+    scores (log2 units, per query head) rises by more than `slack` past its
+    previous value: a lower bound on the rescales a kernel with that slack
+    performs."""
+    indptr, ind, last, sub, sub_scales = compact(meta, pool, [b], scales)
+    k, _ = O.gather_pages(sub, indptr, ind, last, 0, sub_scales)
+    hq, d = q.shape[1], q.shape[2]
+    g = hq // k.shape[1]
+    sc = (1.0 / math.sqrt(d)) if sm_scale is None else sm_scale
+    qq = q[b].float().cpu()
+    s = torch.einsum("hd,lhd->hl", qq, k.repeat_interleave(g, 1)) * sc / math.log(2.0)
+    jumps = 0
+    for h in range(hq):
+        m = -math.inf
+        for lo in range(0, s.shape[1], 16):
+            pm = float(s[h, lo:lo + 16].max())
+            if pm > m + slack:
+                if m != -math.inf:
+                    jumps += 1
+                m = pm
+    return jumps
+
+
 def lse_err(lse, ref, rows=None):
     a = lse.float().cpu()
     if rows is not None:

@@ -14,14 +14,17 @@ import pagedattn
 from pagedattn import workloads as W
 from pagedattn.metadata import decode_metadata
 
-from paged_cases import (decode_case, i32, lse_err, max_err, oracle_decode, random_tables,
-                         run_decode, workspace)
+from paged_cases import (decode_case, i32, log2_max_jumps, lse_err, max_err, oracle_decode,
+                         random_tables, rel_err, run_decode, scale_keys_by_page, workspace)
 
 pytestmark = pytest.mark.gpu
 
 TOL_BF16 = 2e-2
 TOL_FP8 = 3e-2
 TOL_LSE = 2e-3
+# error relative to the row's largest reference value (paged_cases.rel_err)
+TOL_REL_BF16 = 2e-2
+TOL_REL_FP8 = 3e-2
 
 EDGE_LENS = [1, 2, 15, 16, 17, 31, 32, 33, 47, 48, 64, 100, 255, 256, 257, 700]
 
@@ -147,6 +150,7 @@ def test_decode_tinyllama_at_scale(gpu):
     out, lse = _fused_append_then_decode(gpu, w, t)
     ref_o, ref_l = oracle_decode(w.meta, t.pool, t.q)
     assert max_err(out, ref_o) <= TOL_BF16
+    assert rel_err(out, ref_o) <= TOL_REL_BF16
     assert lse_err(lse, ref_l) <= TOL_LSE
     # size-independent: every split-KV partition gives the same answer
     ws = workspace(gpu)
@@ -156,6 +160,7 @@ def test_decode_tinyllama_at_scale(gpu):
                 q_data_type=t.q.dtype, split_pages=split)
         o2 = dw.run(t.q, t.pool)
         assert float((o2.float() - out.float()).abs().max()) <= 1e-2, split
+        assert rel_err(o2, out.float().cpu()) <= TOL_REL_BF16, split
 
 
 def test_decode_long_context_split(gpu):
@@ -164,9 +169,12 @@ def test_decode_long_context_split(gpu):
     w = W.llama3_8b_long_decode(seed=0)
     t = W.materialize(w, gpu)
     out, lse = _fused_append_then_decode(gpu, w, t)  # 4096-token chunks
-    subset = [0, 7, 19]
+    lens = w.meta.seq_lens
+    subset = sorted({0, 7, 19, int(np.argmax(lens))})
     ref_o, ref_l = oracle_decode(w.meta, t.pool, t.q, batch=subset)
     assert max_err(out, ref_o, rows=subset) <= TOL_BF16
+    # |o| is ~0.02 at these lengths: the relative bound is the one that bites
+    assert rel_err(out, ref_o, rows=subset) <= TOL_REL_BF16
     assert lse_err(lse, ref_l, rows=subset) <= TOL_LSE
     ws = workspace(gpu)
     dw = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
@@ -174,6 +182,7 @@ def test_decode_long_context_split(gpu):
             q_data_type=t.q.dtype, split_pages=0)
     o_auto, l_auto = dw.run(t.q, t.pool, return_lse=True)
     assert float((o_auto.float() - out.float()).abs().max()) <= 1e-2
+    assert rel_err(o_auto, out.float().cpu()) <= TOL_REL_BF16
     assert float((l_auto - lse).abs().max()) <= 1e-3
 
 
@@ -294,3 +303,142 @@ def test_decode_rope_append_equals_separate(gpu, d, hq, hkv, fp8):
     torch.cuda.synchronize()
     assert torch.equal(o_def, o_exp)
     assert np.array_equal(O.to_bits(pc_), O.to_bits(pd_))
+
+
+def test_decode_llama3_70b_e4m3_workload(gpu):
+    # the 70B-shaped e4m3 decode batch exactly as the benchmark times it:
+    # fused e4m3 append at kv_len - 1 with the page's fixed scale, then
+    # attention under the planner's balanced split; oracle on a seeded subset
+    # that includes the longest sequences, every split over all 128
+    dec, _ = W.llama3_70b_mixed_fp8(seed=0)
+    t = W.materialize(dec, gpu)
+    t.pool, t.scales = pagedattn.quantize_pages_e4m3(t.pool)
+    before = O.to_bits(t.pool)
+    ws = workspace(gpu)
+    dw = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    dw.plan(t.kv_indptr, t.kv_indices, t.kv_last_page_len, dec.hq, dec.hkv, dec.d, 16,
+            q_data_type=t.q.dtype, split_pages=dec.split_pages)
+    out, lse = dw.run(t.q, t.pool, kv_scales=t.scales, return_lse=True, append_key=t.k_new,
+                      append_value=t.v_new)
+    torch.cuda.synchronize()
+    m = dec.meta
+    want, skipped = O.append_pages_e4m3(before, t.scales.cpu(), t.k_new.cpu().float(),
+                                        t.v_new.cpu().float(), m.batch_indices, m.positions,
+                                        m.kv_indices, m.kv_indptr)
+    assert skipped == 0
+    assert np.array_equal(O.to_bits(t.pool), want)
+    # the counter at byte 0 of the workspace holds the clamped pieces
+    clamped = O.e4m3_clamped_pieces(t.k_new.cpu().float(), t.v_new.cpu().float(),
+                                    t.scales.cpu(), m.batch_indices, m.positions,
+                                    m.kv_indices, m.kv_indptr, dec.num_pages)
+    assert int(ws[:4].view(torch.int32).item()) == clamped
+    lens = m.seq_lens
+    rng = np.random.default_rng(70)
+    subset = sorted(set(np.argsort(lens)[-3:].tolist()) |
+                    set(rng.choice(len(lens), 4, replace=False).tolist()))
+    ref_o, ref_l = oracle_decode(m, t.pool, t.q, scales=t.scales, batch=subset)
+    assert max_err(out, ref_o, rows=subset) <= TOL_FP8
+    assert rel_err(out, ref_o, rows=subset) <= TOL_REL_FP8
+    assert lse_err(lse, ref_l, rows=subset) <= TOL_LSE
+    # (8-page chunks would need more than the engine's 128 MiB workspace here)
+    for split in (-1, 0, 32, 256):
+        w2 = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+        w2.plan(t.kv_indptr, t.kv_indices, t.kv_last_page_len, dec.hq, dec.hkv, dec.d, 16,
+                q_data_type=t.q.dtype, split_pages=split)
+        o2, l2 = w2.run(t.q, t.pool, kv_scales=t.scales, return_lse=True)
+        assert float((o2.float() - out.float()).abs().max()) <= 1e-2, split
+        assert rel_err(o2, out.float().cpu()) <= TOL_REL_FP8, split
+        assert float((l2 - lse).abs().max()) <= 1e-3, split
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("d,hq,hkv", [(64, 32, 4), (128, 64, 8)])
+def test_decode_rescale_branch(gpu, fp8, d, hq, hkv):
+    # scores that keep growing page after page (K of page i scaled by
+    # 1 + i/4): the running max moves by more than the lazy-rescale slack
+    # (8 in log2 units) many times per sequence, so O and l are rescaled
+    # from a finite max and split pieces merge with different maxima
+    lens = [1, 17, 300, 700, 1500, 2500]
+    meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=61 + d)
+    pool = scale_keys_by_page(pool, meta, 0.25)
+    q = (q.float() * 2.0).to(q.dtype)
+    scales = None
+    if fp8:
+        pool, scales = pagedattn.quantize_pages_e4m3(pool)
+    assert log2_max_jumps(meta, pool, q, len(lens) - 1, scales=scales) >= 3 * hq
+    tol, tol_rel = (TOL_FP8, TOL_REL_FP8) if fp8 else (TOL_BF16, TOL_REL_BF16)
+    ref_o, ref_l = oracle_decode(meta, pool, q, scales=scales)
+    lse_tol = TOL_LSE + 2e-5 * float(ref_l[torch.isfinite(ref_l)].abs().max())
+    ws = workspace(gpu)
+    for split in (-1, 0, 8):
+        out, lse = run_decode(gpu, meta, pool, q, hq, hkv, d, split_pages=split,
+                              kv_scales=scales, ws=ws)
+        assert max_err(out, ref_o) <= tol, split
+        assert rel_err(out, ref_o) <= tol_rel, split
+        assert lse_err(lse, ref_l) <= lse_tol, split
+    # device-side partition
+    w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    w.plan(i32(meta.kv_indptr, gpu), i32(meta.kv_indices, gpu), i32(meta.kv_last_page_len, gpu),
+           hq, hkv, d, 16, q_data_type=q.dtype, device_plan=True)
+    out, lse = w.run(q, pool, kv_scales=scales, return_lse=True)
+    torch.cuda.synchronize()
+    assert rel_err(out, ref_o) <= tol_rel
+    assert lse_err(lse, ref_l) <= lse_tol
+    # fused append of a new token whose K row is larger still
+    g = torch.Generator(device=gpu)
+    g.manual_seed(62)
+    kn = (torch.randn((len(lens), hkv, d), generator=g, device=gpu) * 30).to(torch.bfloat16)
+    vn = torch.randn((len(lens), hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+    pa = pool.clone()
+    w8 = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    w8.plan(i32(meta.kv_indptr, gpu), i32(meta.kv_indices, gpu),
+            i32(meta.kv_last_page_len, gpu), hq, hkv, d, 16, q_data_type=q.dtype,
+            split_pages=8)
+    o_f = w8.run(q, pa, kv_scales=scales, append_key=kn, append_value=vn)
+    torch.cuda.synchronize()
+    ref_f, _ = oracle_decode(meta, pa, q, scales=scales)
+    assert rel_err(o_f, ref_f) <= tol_rel
+
+
+def test_decode_fused_append_counts(gpu):
+    # the fused e4m3 append counts what the stand-alone append counts:
+    # clamped pieces (rows past +-448 x scale, a zero or infinite page
+    # scale) and new tokens outside their sequence's pages, in the int32 at
+    # byte 0 of the workspace; the pool bytes equal the oracle's
+    d, hq, hkv = 128, 64, 8
+    lens = [5, 16, 17, 40, 100, 333]
+    meta, pool16, q = decode_case(gpu, lens, hq, hkv, d, seed=71)
+    pool, scales = pagedattn.quantize_pages_e4m3(pool16)
+    bsz = len(lens)
+    g = torch.Generator(device=gpu)
+    g.manual_seed(72)
+    kn = (torch.randn((bsz, hkv, d), generator=g, device=gpu) * 8).to(torch.bfloat16)
+    vn = torch.randn((bsz, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+    last_pages = [int(meta.kv_indices[meta.kv_indptr[b + 1] - 1]) for b in range(bsz)]
+    scales[last_pages[1], 0, 3] = 0.0
+    scales[last_pages[4], 1, 0] = float("inf")
+    pos = np.asarray(lens, np.int64) - 1
+    pos[2] = lens[2] + 40  # past the sequence's pages: skipped and counted
+    before = O.to_bits(pool)
+    ka = kn.clone()
+    qa = q.clone()
+    pagedattn.apply_rope_pos_ids_inplace(qa, ka, i32(pos, gpu), rope_theta=1e4, rope_scale=1.0)
+    bi = np.arange(bsz)
+    want, skipped = O.append_pages_e4m3(before, scales.cpu(), ka.cpu().float(),
+                                        vn.cpu().float(), bi, pos, meta.kv_indices,
+                                        meta.kv_indptr)
+    clamped = O.e4m3_clamped_pieces(ka.cpu().float(), vn.cpu().float(), scales.cpu(), bi, pos,
+                                    meta.kv_indices, meta.kv_indptr, pool.shape[0])
+    assert skipped == 1 and clamped > 2 * (d // 8)
+    for split in (-1, 0, 8):
+        ws = workspace(gpu)
+        w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+        w.plan(i32(meta.kv_indptr, gpu), i32(meta.kv_indices, gpu),
+               i32(meta.kv_last_page_len, gpu), hq, hkv, d, 16, q_data_type=q.dtype,
+               split_pages=split)
+        pb = pool.clone()
+        w.run(q, pb, kv_scales=scales, append_key=kn, append_value=vn, rope=(1.0, 1e4),
+              positions=i32(pos, gpu))
+        torch.cuda.synchronize()
+        assert np.array_equal(O.to_bits(pb), want), split
+        assert int(ws[:4].view(torch.int32).item()) == skipped + clamped, split

@@ -129,6 +129,50 @@ def test_append_e4m3_bit_exact(gpu, src):
     assert np.array_equal(O.to_bits(q8), want)
 
 
+@pytest.mark.parametrize("src", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("with_rope", [False, True])
+def test_append_e4m3_fixed_scale_counts(gpu, src, with_rope):
+    # fixed-scale e4m3 appends (stand-alone and RoPE-fused) count every
+    # skipped token and every clamped 8-element piece in error_flag; blocks
+    # with a zero or infinite scale get zero codes and are counted too
+    meta, pool, k, v = _append_case(gpu, src, 16, True)
+    q8, scales = pagedattn.quantize_pages_e4m3(pool)
+    pages = meta.kv_indices
+    scales[int(pages[0]), 0, 1] = 0.0
+    scales[int(pages[3]), 1, 2] = float("inf")
+    k = (k.float() * 40).to(src)
+    bi = meta.batch_indices.copy()
+    pos = meta.positions.copy()
+    bi[5] = 999
+    pos[7] = -1
+    g = torch.Generator(device=gpu)
+    g.manual_seed(17)
+    q = torch.randn((meta.nnz, 8, k.shape[2]), generator=g, device=gpu).to(src)
+    before = O.to_bits(q8)
+    ka = k.clone()
+    if with_rope:
+        qa = q.clone()
+        pagedattn.apply_rope_pos_ids_inplace(qa, ka, i32(pos, gpu), rope_theta=1e4,
+                                             rope_scale=1.0)
+    want, skipped = O.append_pages_e4m3(before, scales.cpu(), ka.cpu().float(), v.cpu().float(),
+                                        bi, pos, meta.kv_indices, meta.kv_indptr)
+    clamped = O.e4m3_clamped_pieces(ka.cpu().float(), v.cpu().float(), scales.cpu(), bi, pos,
+                                    meta.kv_indices, meta.kv_indptr, q8.shape[0])
+    assert skipped == 2 and clamped > 2 * (k.shape[2] // 8)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    args = (i32(bi, gpu), i32(pos, gpu), q8, i32(meta.kv_indices, gpu),
+            i32(meta.kv_indptr, gpu), i32(meta.kv_last_page_len, gpu))
+    if with_rope:
+        pagedattn.rope_append_paged_kv_cache(q, k, v, *args, kv_layout="HND", rope_scale=1.0,
+                                             rope_theta=1e4, kv_scales=scales, error_flag=err)
+    else:
+        pagedattn.append_paged_kv_cache(k, v, *args, kv_layout="HND", kv_scales=scales,
+                                        error_flag=err)
+    torch.cuda.synchronize()
+    assert np.array_equal(O.to_bits(q8), want)
+    assert int(err.item()) == skipped + clamped
+
+
 def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
     e = torch.floor(torch.log2(x.abs().clamp_min(2.0 ** -100)))
     return torch.pow(2.0, e - 7)
@@ -195,4 +239,10 @@ def test_rope_append_equals_separate(gpu, dtype, prefill, fp8):
     assert torch.equal(q_a, q_b)
     assert torch.equal(k_a, k_b)
     assert np.array_equal(O.to_bits(pool_a), O.to_bits(pool_b))
-    assert int(err_a.item()) == int(err_b.item()) == 1
+    # the skipped token, plus (e4m3) the 8-element pieces clamped at +-448:
+    # new rows are not bounded by the pool's per-page amax scales
+    clamped = 0
+    if fp8:
+        clamped = O.e4m3_clamped_pieces(k_a.cpu().float(), v.cpu().float(), scales.cpu(), bi,
+                                        pos, meta.kv_indices, meta.kv_indptr, pool.shape[0])
+    assert int(err_a.item()) == int(err_b.item()) == 1 + clamped

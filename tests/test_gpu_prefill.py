@@ -11,13 +11,17 @@ import pagedattn
 from pagedattn import workloads as W
 
 from paged_cases import (i32, lse_err, max_err, oracle_prefill, oracle_prefill_rows,
-                         prefill_case, run_decode, run_prefill, workspace)
+                         prefill_case, rel_err, run_decode, run_prefill, scale_keys_by_page,
+                         workspace)
 
 pytestmark = pytest.mark.gpu
 
 TOL_BF16 = 2e-2
 TOL_FP8 = 3e-2
 TOL_LSE = 2e-3
+# error relative to the row's largest reference value (paged_cases.rel_err)
+TOL_REL_BF16 = 2e-2
+TOL_REL_FP8 = 3e-2
 
 # (cached prefix, new chunk) pairs: empty prefix, partial pages, exact pages,
 # single-token chunks, chunks longer than a row tile
@@ -72,6 +76,7 @@ def test_prefill_llama3_8b_chunked(gpu):
     out, lse = run_prefill(gpu, m, t.pool, t.q, w.hq, w.hkv, w.d)
     ref_o, ref_l = oracle_prefill(m, t.pool, t.q)
     assert max_err(out, ref_o) <= TOL_BF16
+    assert rel_err(out, ref_o) <= TOL_REL_BF16
     assert lse_err(lse, ref_l) <= TOL_LSE
 
 
@@ -112,4 +117,28 @@ def test_prefill_e4m3_mixed(gpu):
                                        scales=t.scales)
             r0 = int(m.qo_indptr[b]) + int(lo)
             assert max_err(out[r0:r0 + 128], o) <= TOL_FP8
+            assert rel_err(out[r0:r0 + 128], o) <= TOL_REL_FP8
             assert lse_err(lse[r0:r0 + 128], l) <= TOL_LSE
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("d,hq,hkv", [(128, 32, 8), (64, 32, 4)])
+def test_prefill_rescale_branch(gpu, fp8, d, hq, hkv):
+    # K of page i scaled by 1 + i/4: every query row's running max moves by
+    # more than the lazy-rescale slack (8 in log2 units) across KV tiles, so
+    # O and l are rescaled from a finite max in the causal multi-tile loop
+    computed = [1000, 0, 512, 2048]
+    chunks = [300, 257, 64, 129]
+    meta, pool, q = prefill_case(gpu, computed, chunks, hq, hkv, d, seed=81 + d)
+    pool = scale_keys_by_page(pool, meta, 0.25)
+    q = (q.float() * 2.0).to(q.dtype)
+    scales = None
+    if fp8:
+        pool, scales = pagedattn.quantize_pages_e4m3(pool)
+    ref_o, ref_l = oracle_prefill(meta, pool, q, scales=scales)
+    lse_tol = TOL_LSE + 2e-5 * float(ref_l[torch.isfinite(ref_l)].abs().max())
+    tol, tol_rel = (TOL_FP8, TOL_REL_FP8) if fp8 else (TOL_BF16, TOL_REL_BF16)
+    out, lse = run_prefill(gpu, meta, pool, q, hq, hkv, d, kv_scales=scales)
+    assert max_err(out, ref_o) <= tol
+    assert rel_err(out, ref_o) <= tol_rel
+    assert lse_err(lse, ref_l) <= lse_tol

@@ -206,6 +206,174 @@ def test_quantize_pages_scale():
     assert bool((err <= bound + 1e-12).all())
 
 
+# fixed-scale e4m3 append and e4m3 gather, pinned element by element: the
+# e4m3fn value of a code is computed from its bit fields, and rounding is a
+# brute-force search for the nearest code (ties to the even mantissa), so
+# neither pin goes through torch's float8 conversion that the oracle uses.
+
+def _e4m3_value(code: int) -> float:
+    """OCP e4m3fn: sign, 4 exponent bits (bias 7), 3 mantissa bits; exponent 0
+    is subnormal (m / 8 * 2^-6); S.1111.111 is NaN; no infinities."""
+    sign = -1.0 if code & 0x80 else 1.0
+    e, m = (code >> 3) & 0xF, code & 0x7
+    if e == 0xF and m == 0x7:
+        return math.nan
+    if e == 0:
+        return sign * (m / 8.0) * 2.0 ** -6
+    return sign * (1.0 + m / 8.0) * 2.0 ** (e - 7)
+
+
+_E4M3_POS = [(_e4m3_value(c), c) for c in range(0x7F)]  # 0 .. 448, increasing
+
+
+def _e4m3_round(y: float) -> int:
+    """Code of the e4m3fn value nearest to y after clamping to +-448; a tie
+    takes the even code (round to nearest even); the sign of y is kept (-0
+    included)."""
+    neg = math.copysign(1.0, y) < 0
+    a = min(abs(y), 448.0)
+    best = None
+    for val, code in _E4M3_POS:
+        d = abs(val - a)
+        if best is None or d < best[0] or (d == best[0] and code % 2 == 0):
+            best = (d, code)
+    return best[1] | (0x80 if neg else 0)
+
+
+def test_e4m3_bitfield_table_matches_torch():
+    # the bit-field decoder itself agrees with the float8 dtype on all 256 codes
+    vals = torch.from_numpy(np.arange(256, dtype=np.uint8)).view(torch.float8_e4m3fn).float()
+    for c in range(256):
+        want = float(vals[c])
+        got = _e4m3_value(c)
+        assert (math.isnan(got) and math.isnan(want)) or got == want, c
+
+
+def _append_e4m3_loop(pool, scales, k, v, bi, pos, ind, indptr, kscale_kind=0, vscale_kind=1,
+                      head_shift=0):
+    """Per-element restatement of the fixed-scale e4m3 append; the keyword
+    arguments plant mistakes (which scale a kind reads, a head offset)."""
+    out = pool.copy()
+    n_pages, _, h_n, _, d = pool.shape
+    skipped = 0
+    clamped = 0
+    for j in range(len(bi)):
+        b, ps = int(bi[j]), int(pos[j])
+        if not (0 <= b < len(indptr) - 1) or ps < 0:
+            skipped += 1
+            continue
+        it = int(indptr[b]) + ps // 16
+        if it >= int(indptr[b + 1]) or it >= len(ind):
+            skipped += 1
+            continue
+        page = int(ind[it])
+        if not (0 <= page < n_pages):
+            skipped += 1
+            continue
+        for kind, src, skind in ((0, k, kscale_kind), (1, v, vscale_kind)):
+            for h in range(h_n):
+                s = np.float32(scales[page, skind, (h + head_shift) % h_n])
+                ok = bool(s > 0) and math.isfinite(float(s))
+                for c0 in range(0, d, 8):
+                    piece_bad = not ok
+                    for t in range(c0, c0 + 8):
+                        if ok:
+                            y = np.float32(np.float32(src[j, h, t]) / s)
+                            piece_bad |= not (abs(float(y)) <= 448.0)
+                            out[page, kind, h, ps % 16, t] = _e4m3_round(float(y))
+                        else:
+                            out[page, kind, h, ps % 16, t] = 0
+                    clamped += int(piece_bad)
+    return out, skipped, clamped
+
+
+def _e4m3_append_case(seed=6):
+    rng = np.random.default_rng(seed)
+    p, h, d = 7, 3, 16
+    pool = rng.integers(0, 256, size=(p, 2, h, 16, d), dtype=np.uint8)
+    pool[pool & 0x7F == 0x7F] = 0  # no NaN codes in the starting pool
+    scales = torch.from_numpy(
+        np.ldexp(1.0, rng.integers(-6, 3, size=(p, 2, h))).astype(np.float32)
+        * rng.choice([1.0, 0.75, 1.3], size=(p, 2, h)).astype(np.float32))
+    scales[2, 1, 0] = 0.0       # a fresh page: zero codes, counted
+    scales[4, 0, 2] = math.inf  # not finite: zero codes, counted
+    indptr = np.array([0, 2, 4, 6], dtype=np.int32)
+    ind = np.array([3, 2, 5, 4, 0, 6], dtype=np.int32)
+    bi = np.array([0, 0, 1, 1, 2, 2, 5, 1], dtype=np.int32)  # batch 5 is out of range
+    pos = np.array([0, 17, 3, 30, 9, 16, 0, 40], dtype=np.int32)  # 40 is past seq 1's pages
+    n = len(bi)
+    k = torch.from_numpy(rng.normal(size=(n, h, d)).astype(np.float32)).to(torch.bfloat16)
+    v = torch.from_numpy(rng.normal(size=(n, h, d)).astype(np.float32)).to(torch.bfloat16)
+    # exact ties of e4m3 rounding and values past the clamp
+    k[0, 0, :4] = torch.tensor([1.0625, 1.1875, -1.0625, 0.0]) * float(scales[3, 0, 0])
+    k[1, 1, 5] = 1000.0 * float(scales[2, 0, 1])
+    v[2, 2, 8] = -600.0 * float(scales[5, 1, 2])
+    return pool, scales, k.float(), v.float(), bi, pos, ind, indptr
+
+
+def test_append_e4m3_loop():
+    pool, scales, k, v, bi, pos, ind, indptr = _e4m3_append_case()
+    want, want_skip, want_clamp = _append_e4m3_loop(pool, scales.numpy(), k.numpy(), v.numpy(),
+                                                    bi, pos, ind, indptr)
+    got, skipped = O.append_pages_e4m3(pool, scales, k, v, bi, pos, ind, indptr)
+    assert skipped == want_skip == 2
+    assert np.array_equal(got, want)
+    clamped = O.e4m3_clamped_pieces(k, v, scales, bi, pos, ind, indptr, pool.shape[0])
+    # two over-range values, a zero scale and an infinite scale (2 pieces each)
+    assert clamped == want_clamp
+    assert clamped >= 2 + 2 + 2
+
+
+def test_gather_e4m3_loop():
+    pool, scales, k, v, bi, pos, ind, indptr = _e4m3_append_case(7)
+    bits, _ = O.append_pages_e4m3(pool, scales, k, v, bi, pos, ind, indptr)
+    last = np.array([16, 16, 7], dtype=np.int32)
+    f8 = torch.from_numpy(bits).view(torch.float8_e4m3fn)
+    for b in range(3):
+        kk, vv = O.gather_pages(f8, indptr, ind, last, b, scales)
+        n_tok = (indptr[b + 1] - indptr[b] - 1) * 16 + last[b]
+        assert kk.shape[0] == n_tok
+        for i in range(n_tok):
+            page = int(ind[indptr[b] + i // 16])
+            for kind, got in ((0, kk), (1, vv)):
+                for h in range(bits.shape[2]):
+                    s = np.float32(scales[page, kind, h])
+                    for t in range(bits.shape[4]):
+                        want = float(np.float32(_e4m3_value(int(bits[page, kind, h, i % 16,
+                                                                          t]))) * s)
+                        g = float(got[i, h, t])
+                        # zero codes times an infinite scale are NaN on both sides
+                        assert g == want or (math.isnan(g) and math.isnan(want)), (b, i, h, t)
+
+
+def test_e4m3_clamped_pieces_loop():
+    pool, scales, k, v, bi, pos, ind, indptr = _e4m3_append_case(8)
+    k = k * 40.0  # many pieces past +-448 * scale
+    _, _, want = _append_e4m3_loop(pool, scales.numpy(), k.numpy(), v.numpy(), bi, pos, ind,
+                                   indptr)
+    assert O.e4m3_clamped_pieces(k, v, scales, bi, pos, ind, indptr, pool.shape[0]) == want > 6
+
+
+def test_e4m3_pins_catch_planted_mistakes():
+    pool, scales, k, v, bi, pos, ind, indptr = _e4m3_append_case()
+    ref, _, _ = _append_e4m3_loop(pool, scales.numpy(), k.numpy(), v.numpy(), bi, pos, ind,
+                                  indptr)
+    # K and V scales swapped, or the scale of the neighbouring head, change bytes
+    for kw in ({"kscale_kind": 1, "vscale_kind": 0}, {"head_shift": 1}, {"head_shift": -1}):
+        bad, _, _ = _append_e4m3_loop(pool, scales.numpy(), k.numpy(), v.numpy(), bi, pos, ind,
+                                      indptr, **kw)
+        assert not np.array_equal(bad, ref), kw
+    # a gather that dequantises with the V scale for K, or head h + 1's scale
+    f8 = torch.from_numpy(ref).view(torch.float8_e4m3fn)
+    last = np.array([16, 16, 16], dtype=np.int32)
+    k0, _ = O.gather_pages(f8, indptr, ind, last, 0, scales)
+    sw = scales[:, [1, 0]].contiguous()
+    k_bad, _ = O.gather_pages(f8, indptr, ind, last, 0, sw)
+    assert not torch.equal(k_bad, k0)
+    k_bad2, _ = O.gather_pages(f8, indptr, ind, last, 0, scales.roll(1, dims=2))
+    assert not torch.equal(k_bad2, k0)
+
+
 # -----------------------------------------------------------------------------
 # attention
 
