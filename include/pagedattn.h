@@ -369,6 +369,32 @@ int pagedattn_quantize_pages_e4m3(const void* src_cache, int32_t src_dtype,
                                   int32_t head_dim, int32_t page_size,
                                   void* stream);
 
+/* ---------------------------------------------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, serving loops or harnesses that
+ * forbid hipMalloc.  pagedattn_decode_run over the device-side partition of
+ * pagedattn_decode_plan_device (the same kernels and partition, so the same
+ * results bit for bit), with no plan object and no workspace: the split
+ * partials live in a static device array of PAGEDATTN_NOALLOC_SCRATCH_BYTES
+ * that every GPU the library runs on holds until the process ends.  The call
+ * allocates nothing (its first call on a device looks up that device's copy
+ * of the array with hipGetSymbolAddress).  The partials of a shape take
+ * 2 x 4 x CUs slots of (Hq/Hkv) x (D + 1) fp32 values; a shape that does not
+ * fit (none of the supported head shapes on a 256-CU MI355X) returns
+ * PAGEDATTN_ERR_WORKSPACE.  Nothing in the array needs to start at zero,
+ * but every call on a GPU shares it, so calls that overlap on one GPU
+ * (different streams, or threads without ordering) race.  Arguments as for
+ * pagedattn_decode_plan_device + pagedattn_decode_run. */
+#define PAGEDATTN_NOALLOC_SCRATCH_BYTES (17u << 20)
+int pagedattn_decode_run_noalloc(int32_t batch_size, int32_t num_qo_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                 const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                                 int32_t q_dtype, const void* paged_kv_cache, int32_t kv_dtype,
+                                 const float* kv_scales, int32_t num_pages,
+                                 const int32_t* kv_indices, int32_t num_indices,
+                                 const int32_t* kv_indptr, const int32_t* kv_last_page_len,
+                                 void* out, float* lse, float sm_scale, void* stream);
+
 /* No counterpart in the reference: a plain streaming copy of `bytes` bytes
  * (multiple of 16, 16-byte aligned pointers), used to calibrate HBM byte
  * counters against a kernel of known traffic. */

@@ -1438,3 +1438,79 @@ int pagedattn_decode_run_rope_append(
 }
 
 }  // extern "C"
+
+// ----------------------------------------------------------------------------
+// Decode without a plan object or workspace (pagedattn_decode_run_noalloc).
+namespace pa {
+
+// Split partials of pagedattn_decode_run_noalloc: one array per GPU, loaded
+// with the code object and held until the process ends.  Host code never
+// uses its name as an address: the per-device address comes from
+// hipGetSymbolAddress.
+static __device__ __align__(256) uint8_t scratch[PAGEDATTN_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kNoAllocMaxDevices = 64;
+struct NoAllocDevice {
+  char* scratch;  // device address of `scratch` on this GPU
+  int cus;
+};
+static NoAllocDevice g_noalloc[kNoAllocMaxDevices];
+static std::mutex g_noalloc_mu;
+
+// Set-up on the current device, once: the address of its copy of the
+// array and its CU count.  Allocates nothing.
+static int noalloc_device(const char* who, NoAllocDevice* out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(PAGEDATTN_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kNoAllocMaxDevices)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: device %d (at most %d devices)", who, dev,
+                     kNoAllocMaxDevices);
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  NoAllocDevice& d = g_noalloc[dev];
+  if (d.scratch == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr)
+      return set_error(PAGEDATTN_ERR_HIP, "%s: hipGetSymbolAddress(scratch): %s", who,
+                       hipGetErrorString(e));
+    int cus = 0;
+    e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess || cus <= 0)
+      return set_error(PAGEDATTN_ERR_HIP, "%s: CU count of device %d: %s", who, dev,
+                       hipGetErrorString(e));
+    d.cus = cus;
+    d.scratch = static_cast<char*>(ptr);
+  }
+  *out = d;
+  return PAGEDATTN_OK;
+}
+
+}  // namespace pa
+
+extern "C" {
+
+int pagedattn_decode_run_noalloc(int32_t batch_size, int32_t num_qo_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                 const void* q, int64_t q_stride_n, int64_t q_stride_h,
+                                 int32_t q_dtype, const void* paged_kv_cache, int32_t kv_dtype,
+                                 const float* kv_scales, int32_t num_pages,
+                                 const int32_t* kv_indices, int32_t num_indices,
+                                 const int32_t* kv_indptr, const int32_t* kv_last_page_len,
+                                 void* out, float* lse, float sm_scale, void* stream) {
+  const char* who = "decode_run_noalloc";
+  NoAllocDevice dev;
+  int rc = noalloc_device(who, &dev);
+  if (rc) return rc;
+  // a stack plan: its host staging vector stays empty, nothing is allocated
+  pagedattn_plan plan;
+  rc = setup_device_plan(who, &plan, batch_size, num_qo_heads, num_kv_heads, head_dim,
+                         page_size, dev.cus, dev.scratch, PAGEDATTN_NOALLOC_SCRATCH_BYTES);
+  if (rc) return rc;
+  return decode_run_impl(who, &plan, q, q_stride_n, q_stride_h, q_dtype, paged_kv_cache,
+                         kv_dtype, kv_scales, num_pages, kv_indices, num_indices, kv_indptr,
+                         kv_last_page_len, out, lse, sm_scale, nullptr, stream);
+}
+
+}  // extern "C"
