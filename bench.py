@@ -5,23 +5,29 @@ into their pages, then paged attention (decode: one query per sequence;
 prefill: ragged causal chunks).  The plan is built once per batch (the engine
 builds it once per forward and reuses it across layers).
 
-Default workload: TinyLlama-1.1B paged decode at scale (32q/4kv heads, D=64,
-page 16, B=256, kv_len U[256,2048], bf16).  `value` is whole-step
-throughput in algorithmic HBM GB/s; `roofline` is the decode attention
-launch (algorithmic bytes / average launch time from HIP events);
-`cpu_baseline` is the fp32 CPU oracle on a bounded sample of the same batch.
-Pools are rotated across replicas totalling > 1 GB so the 256 MB Infinity
-Cache cannot hold the KV between steps.
+Headline (`value`): TinyLlama-1.1B paged decode at scale (32q/4kv heads,
+D=64, page 16, B=256, kv_len U[256,2048], bf16), whole-step throughput in
+algorithmic HBM GB/s.  Every configuration is timed step by step with HIP
+events on the launch stream (median of >= 20 steps) over pools rotated
+across replicas totalling > 512 MB, so the 256 MB Infinity Cache cannot hold
+the KV between steps.  Each configuration carries a `roofline` block (HBM
+GB/s against 8 TB/s for decode, TFLOP/s against the 2.5 PFLOP/s bf16 dense
+MFMA peak for prefill; `traffic` from the committed rocprofv3 FETCH_SIZE /
+WRITE_SIZE summaries when they match the built sources) and a
+`cpu_baseline` (the fp32 CPU oracle on a bounded, stated sample).
 
 Prints ONE JSON line.  `--gpus N` with N > 1 exits: this build runs on one GPU.
+`--config` runs a subset (for profiling runs), e.g. `--config c4 --no-cpu`.
 """
 
 from __future__ import annotations
 
 import argparse
 import dataclasses
+import hashlib
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -33,10 +39,24 @@ for _p in (os.path.join(ROOT, "llm-inference-runtime_amd"), ROOT):
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 WS_BYTES = 128 << 20
+CONFIGS = ("c2", "c3", "c4", "c4b", "c5d", "c5p", "devplan", "kvwrite")
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+CSRC = os.path.join(ROOT, "llm-inference-runtime_amd", "csrc")
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def sources_sha() -> str:
+    """Hash of the kernel sources; a committed traffic figure applies only
+    to the sources it was measured with."""
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(CSRC)):
+        if name.endswith((".hip", ".h", ".cpp")):
+            with open(os.path.join(CSRC, name), "rb") as f:
+                h.update(name.encode() + b"\0" + f.read())
+    return h.hexdigest()[:16]
 
 
 def _replicas(bytes_per_instance: int, min_total: int = 1 << 30, cap: int = 8) -> int:
@@ -46,8 +66,133 @@ def _replicas(bytes_per_instance: int, min_total: int = 1 << 30, cap: int = 8) -
     return r
 
 
-def bench_decode(w, args, dev, dtype, label, cpu_sample: int = 0):
-    import numpy as np
+_busy = None
+
+
+def _fill_queue(ms: float = 3.0) -> None:
+    """Puts a few ms of streaming copies on the stream, so that the host has
+    queued every timed step before the GPU reaches them: the event pairs
+    then time the device, not the Python launch path."""
+    import torch
+
+    import pagedattn
+    global _busy
+    if _busy is None:
+        n = 256 << 20
+        _busy = (torch.empty(n, dtype=torch.uint8, device="cuda"),
+                 torch.empty(n, dtype=torch.uint8, device="cuda"))
+    for _ in range(max(1, int(ms / 0.11))):  # ~0.11 ms per 256 MiB copy
+        pagedattn.copy_bytes(_busy[1], _busy[0])
+
+
+def time_steps(fn, steps: int, warmup: int) -> list[float]:
+    """Per-step device time (ms): a HIP event pair around every call, on the
+    stream the library launches on (torch's current stream), with the steps
+    queued behind a few ms of other work (_fill_queue)."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(steps)]
+    torch.cuda.synchronize()
+    _fill_queue(0.15 * steps + 1.0)
+    for i, (a, b) in enumerate(evs):
+        a.record()
+        fn(warmup + i)
+        b.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in evs]
+
+
+def _stats(ms: list[float]) -> dict:
+    return {"ms_median": statistics.median(ms), "ms_mean": statistics.fmean(ms),
+            "ms_min": min(ms), "ms_max": max(ms), "iterations": len(ms)}
+
+
+def _time_graph_ms(fn, steps: int, warmup: int) -> float:
+    """Device time per call of fn: `steps` calls captured in one HIP graph,
+    replayed and timed, so the host's per-call argument checks (tens of us
+    for a small launch) stay out of the figure."""
+    import torch
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(warmup):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(steps):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            return next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
+                        "unknown")
+    except OSError:
+        return "unknown"
+
+
+def _cpu_time(fn, min_reps: int = 3, budget_s: float = 8.0) -> tuple[float, int, float]:
+    """Median seconds of fn over at least min_reps passes (more while the
+    budget lasts)."""
+    import torch
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    times = []
+    while len(times) < min_reps or (sum(times) < budget_s and len(times) < 200):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times), sum(times)
+
+
+def load_traffic(workload: str) -> dict:
+    """HBM bytes per step measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    (scaled by the plain-copy calibration), as committed in
+    profiles/hbm_traffic.json; null when absent or measured on other sources."""
+    try:
+        with open(TRAFFIC_JSON) as f:
+            d = json.load(f)
+    except (OSError, ValueError):
+        return {"traffic": None, "traffic_note": "no committed counter profile"}
+    e = d.get("workloads", {}).get(workload)
+    if e is None:
+        return {"traffic": None, "traffic_note": "no committed counter profile"}
+    if d.get("sources_sha") != sources_sha():
+        return {"traffic": None,
+                "traffic_note": "committed counter profile was measured on other kernel sources"}
+    return {"traffic": e["traffic_bytes_per_step"],
+            "traffic_source": os.path.relpath(TRAFFIC_JSON, ROOT)}
+
+
+def roofline(bound: str, kernel: str, achieved: float, work: int, ms: float,
+             workload: str) -> dict:
+    peak = HBM_PEAK_GBS if bound == "hbm" else BF16_PEAK_TFLOPS
+    r = {"bound": bound, "kernel": kernel, "achieved": round(achieved, 2), "peak": peak,
+         "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(achieved / peak, 4)}
+    r.update(load_traffic(workload))
+    r["alg_bytes_per_launch" if bound == "hbm" else "alg_flops_per_launch"] = work
+    r["launch_ms_median"] = round(ms, 5)
+    return r
+
+
+# -----------------------------------------------------------------------------
+# decode
+
+def bench_decode(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
+                 kernel: str) -> dict:
     import torch
 
     import pagedattn
@@ -79,144 +224,172 @@ def bench_decode(w, args, dev, dtype, label, cpu_sample: int = 0):
             for _ in range(reps)]
 
     def step(i):
-        # the decode step: new token's K/V appended at kv_len - 1, then
-        # attention, in one launch (pagedattn_decode_run_append) plus the
-        # split-KV merge launch when the plan cut sequences
+        # the decode step: each sequence's new K/V appended at kv_len - 1,
+        # then attention, in one launch (pagedattn_decode_run_append), plus
+        # the split-KV merge launch when the plan cut sequences
         t = inst[i % reps]
         dw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps], append_key=t.k_new,
                append_value=t.v_new)
 
-    for i in range(args.warmup):
-        step(i)
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(args.steps):
-        step(args.warmup + i)
-    end.record()
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    attn_avg = total_ms / args.steps
+    st = _stats(time_steps(step, args.steps, args.warmup))
+    ms = st["ms_median"]
     res = {
         "workload": label,
-        "ms_per_step": total_ms / args.steps,
-        "step_GBps": alg_step / (total_ms / args.steps * 1e-3) / 1e9,
-        "attn_ms_avg": attn_avg,
-        "attn_GBps": alg_attn / (attn_avg * 1e-3) / 1e9,
-        "alg_bytes_attn": alg_attn,
+        **{k: round(v, 5) if isinstance(v, float) else v for k, v in st.items()},
+        "step_GBps": alg_step / (ms * 1e-3) / 1e9,
         "alg_bytes_step": alg_step,
+        "alg_bytes_attn": alg_attn,
         "plan_ms_host": plan_ms,
         "replicas": reps,
         "batch": w.meta.batch_size,
         "kv_tokens": int(w.meta.seq_lens.sum()),
         "split_pages": w.split_pages,
     }
-    res["attn_frac"] = res["attn_GBps"] / HBM_PEAK_GBS
-    if cpu_sample:
-        res["cpu"] = cpu_decode_baseline(w, inst[0], cpu_sample, kv_elem)
+    res["frac"] = res["step_GBps"] / HBM_PEAK_GBS
+    res["roofline"] = roofline("hbm", kernel, res["step_GBps"], alg_step, ms, label)
+    if cpu_seqs is not None:
+        res["cpu_baseline"] = cpu_decode_baseline(w, inst[0], cpu_seqs, kv_elem)
     del inst, outs
     torch.cuda.empty_cache()
     return res
 
 
-def bench_prefill(w, args, dev, dtype, label):
+def cpu_decode_baseline(w, t, rows: list[int], kv_elem: int) -> dict:
+    """fp32 oracle decode over the sequences `rows` of the batch (the pool
+    pages they use copied to the host beforehand, untimed)."""
     import numpy as np
+    import torch
+
+    import oracle as O
+
+    m = w.meta
+    parts = [m.kv_indices[m.kv_indptr[b]:m.kv_indptr[b + 1]] for b in rows]
+    pages = np.concatenate(parts)
+    indptr = np.concatenate([[0], np.cumsum([len(p) for p in parts])]).astype(np.int32)
+    idx = torch.from_numpy(pages.astype(np.int64)).to(t.pool.device)
+    sub = t.pool.index_select(0, idx).cpu()
+    scales = None if t.scales is None else t.scales.index_select(0, idx).cpu()
+    q = t.q[rows].float().cpu()
+    ind = np.arange(len(pages), dtype=np.int32)
+    last = m.kv_last_page_len[rows]
+    sec, n, total = _cpu_time(lambda: O.decode(q, sub, indptr, ind, last, scales=scales))
+    kv_tok = int(m.seq_lens[rows].astype(np.int64).sum())
+    byts = kv_tok * w.hkv * w.d * 2 * kv_elem + len(rows) * w.hq * w.d * 4
+    cores = len(os.sched_getaffinity(0))
+    subset = "all" if len(rows) == m.batch_size else "a seeded subset of"
+    return {
+        "value": round(byts / sec / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+        "seconds_median": round(sec, 4),
+        "sample": (f"{subset} {len(rows)} of {m.batch_size} sequences of {w.name} "
+                   f"({kv_tok} kv tokens), fp32 torch oracle decode, median of {n} passes "
+                   f"({total:.1f} s) on {cores} threads of {cpu_model()}"),
+    }
+
+
+# -----------------------------------------------------------------------------
+# prefill
+
+def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
+                  kernel: str) -> dict:
     import torch
 
     import pagedattn
     from pagedattn import workloads as W
 
     flops = W.prefill_flops(w)
-    t = W.materialize(w, dev, dtype)
-    if w.fp8:
-        t.pool, t.scales = pagedattn.quantize_pages_e4m3(t.pool)
+    kv_elem = 1 if w.fp8 else 2
+    inst_bytes = (w.num_pages * 2 * w.hkv * 16 * w.d * kv_elem
+                  + w.meta.nnz * w.hq * w.d * 2 * 2)
+    reps = _replicas(inst_bytes, min_total=512 << 20)
+    log(f"{label}: {w.meta.nnz} rows, {flops / 1e9:.1f} GFLOP, replicas={reps}")
+    inst = []
+    for r in range(reps):
+        t = W.materialize(w, dev, dtype, seed=w.seed * 100 + r)
+        if w.fp8:
+            t.pool, t.scales = pagedattn.quantize_pages_e4m3(t.pool)
+        inst.append(t)
     ws = torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
     pw = pagedattn.BatchPrefillWithPagedKVCacheWrapper(ws, "HND")
-    pw.plan(t.qo_indptr, t.kv_indptr, t.kv_indices, t.kv_last_page_len, w.hq, w.hkv, w.d, 16,
-            q_data_type=dtype, causal=True)
-    out = torch.empty_like(t.q)
+    t0 = inst[0]
+    pw.plan(t0.qo_indptr, t0.kv_indptr, t0.kv_indices, t0.kv_last_page_len, w.hq, w.hkv, w.d,
+            16, q_data_type=dtype, causal=True)
+    outs = [torch.empty_like(t.q) for t in inst]
 
-    def step():
+    def step(i):
+        t = inst[i % reps]
         pagedattn.append_paged_kv_cache(t.k_new, t.v_new, t.batch_indices, t.positions, t.pool,
                                         t.kv_indices, t.kv_indptr, t.kv_last_page_len,
                                         kv_layout="HND", kv_scales=t.scales)
-        pw.run(t.q, t.pool, kv_scales=t.scales, out=out)
+        pw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps])
 
-    for _ in range(args.warmup):
-        step()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(args.steps):
-        step()
-    end.record()
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(end)
-    # attention launches back to back: HIP events around the loop
-    start.record()
-    for _ in range(args.steps):
-        pw.run(t.q, t.pool, kv_scales=t.scales, out=out)
-    end.record()
-    torch.cuda.synchronize()
-    avg = start.elapsed_time(end) / args.steps
+    def attn(i):
+        t = inst[i % reps]
+        pw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps])
+
+    st_step = _stats(time_steps(step, args.steps, args.warmup))
+    st = _stats(time_steps(attn, args.steps, args.warmup))
+    ms = st["ms_median"]
     res = {
         "workload": label,
-        "ms_per_step": total_ms / args.steps,
-        "attn_ms_avg": avg,
-        "attn_TFLOPs": flops / (avg * 1e-3) / 1e12,
+        **{k: round(v, 5) if isinstance(v, float) else v for k, v in st.items()},
+        "step_ms_median": round(st_step["ms_median"], 5),
+        "attn_TFLOPs": flops / (ms * 1e-3) / 1e12,
         "alg_flops_attn": flops,
         "rows": int(w.meta.nnz),
         "kv_tokens": int(w.meta.seq_lens.sum()),
+        "replicas": reps,
     }
-    res["attn_frac"] = res["attn_TFLOPs"] / BF16_PEAK_TFLOPS
-    del t, out
+    res["frac"] = res["attn_TFLOPs"] / BF16_PEAK_TFLOPS
+    res["roofline"] = roofline("mfma", kernel, res["attn_TFLOPs"], flops, ms, label)
+    if cpu_seqs is not None:
+        res["cpu_baseline"] = cpu_prefill_baseline(w, inst[0], cpu_seqs)
+    del inst, outs
     torch.cuda.empty_cache()
     return res
 
 
-def _time_ms(fn, steps: int, warmup: int) -> float:
+def cpu_prefill_baseline(w, t, rows: list[int]) -> dict:
+    """fp32 oracle prefill of the sequences `rows` (their chunks over their
+    whole cached prefixes)."""
+    import numpy as np
     import torch
-    for i in range(warmup):
-        fn(i)
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(steps):
-        fn(warmup + i)
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+
+    import oracle as O
+    from pagedattn import workloads as W
+
+    m = w.meta
+    parts = [m.kv_indices[m.kv_indptr[b]:m.kv_indptr[b + 1]] for b in rows]
+    pages = np.concatenate(parts)
+    kv_indptr = np.concatenate([[0], np.cumsum([len(p) for p in parts])]).astype(np.int32)
+    idx = torch.from_numpy(pages.astype(np.int64)).to(t.pool.device)
+    sub = t.pool.index_select(0, idx).cpu()
+    scales = None if t.scales is None else t.scales.index_select(0, idx).cpu()
+    qo = np.diff(m.qo_indptr)
+    q = torch.cat([t.q[int(m.qo_indptr[b]):int(m.qo_indptr[b + 1])] for b in rows]).float().cpu()
+    qo_indptr = np.concatenate([[0], np.cumsum(qo[rows])]).astype(np.int32)
+    ind = np.arange(len(pages), dtype=np.int32)
+    last = m.kv_last_page_len[rows]
+    sec, n, total = _cpu_time(
+        lambda: O.prefill(q, qo_indptr, sub, kv_indptr, ind, last, causal=True, scales=scales),
+        budget_s=4.0)
+    sw = dataclasses.replace(w, meta=dataclasses.replace(
+        m, qo_indptr=qo_indptr, kv_indptr=kv_indptr, kv_indices=ind, kv_last_page_len=last,
+        seq_lens=m.seq_lens[rows]))
+    flops = W.prefill_flops(sw)
+    cores = len(os.sched_getaffinity(0))
+    subset = "all" if len(rows) == m.batch_size else "a seeded subset of"
+    return {
+        "value": round(flops / sec / 1e9, 2), "unit": "GFLOP/s", "cores": cores, "kind": "port",
+        "seconds_median": round(sec, 4),
+        "sample": (f"{subset} {len(rows)} of {m.batch_size} sequences of {w.name} "
+                   f"({int(qo[rows].sum())} query rows, {flops / 1e9:.1f} GFLOP), fp32 torch "
+                   f"oracle prefill, median of {n} passes ({total:.1f} s) on {cores} threads "
+                   f"of {cpu_model()}"),
+    }
 
 
-def _time_graph_ms(fn, steps: int, warmup: int) -> float:
-    """Device time per call of fn: `steps` calls captured in one HIP graph,
-    replayed and timed, so the host's per-call argument checks (tens of us
-    for a small launch) stay out of the figure."""
-    import torch
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for i in range(warmup):
-            fn(i)
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for i in range(steps):
-            fn(i)
-    g.replay()
-    torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    g.replay()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
-
+# -----------------------------------------------------------------------------
+# device plan, KV write path, calibration
 
 def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
     """The same fused decode step with the device-side partition
@@ -229,7 +402,7 @@ def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
     from pagedattn import workloads as W
 
     alg_step = W.decode_bytes(w, 2, with_append=True)
-    reps = _replicas(w.num_pages * 2 * w.hkv * 16 * w.d * 2)
+    reps = _replicas(w.num_pages * 2 * w.hkv * 16 * w.d * 2, min_total=512 << 20)
     inst = [W.materialize(w, dev, dtype, seed=w.seed * 100 + r) for r in range(reps)]
     ws = torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
     out = torch.empty((w.meta.batch_size, w.hq, w.d), dtype=dtype, device=dev)
@@ -241,7 +414,7 @@ def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
     def step(t):
         dw.run(t.q, t.pool, out=out, append_key=t.k_new, append_value=t.v_new)
 
-    eager_ms = _time_ms(lambda i: step(inst[i % reps]), steps, warmup)
+    eager_ms = statistics.median(time_steps(lambda i: step(inst[i % reps]), steps, warmup))
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -255,11 +428,10 @@ def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
         with torch.cuda.graph(g):
             step(t)
         graphs.append(g)
-    graph1_ms = _time_ms(lambda i: graphs[i % reps].replay(), steps, warmup)
+    graph1_ms = statistics.median(time_steps(lambda i: graphs[i % reps].replay(), steps, warmup))
     # an engine captures a whole forward (every layer's call) in one graph:
     # `steps` calls in one graph spread the graph launch over them
     graph_ms = _time_graph_ms(lambda i: step(inst[i % reps]), steps, warmup)
-    # metadata of the batch from a block table on the device
     m = w.meta
     npg = np.diff(m.kv_indptr)
     tables = np.full((m.batch_size, int(npg.max())), -1, dtype=np.int32)
@@ -290,7 +462,7 @@ def bench_kv_write(dev, steps: int = 20, warmup: int = 3) -> dict:
     import torch
 
     import pagedattn
-    from pagedattn.metadata import prefill_metadata
+    from pagedattn.metadata import decode_metadata, prefill_metadata
 
     rng = np.random.default_rng(7)
     hkv, d = 8, 128
@@ -319,8 +491,6 @@ def bench_kv_write(dev, steps: int = 20, warmup: int = 3) -> dict:
     app_ms = _time_graph_ms(lambda i: pagedattn.append_paged_kv_cache_e4m3_amax(
         k, v, bi, pos, q8, ind, indptr, last, scales, kv_layout="HND"), steps, warmup)
     app_bytes = meta.nnz * hkv * d * 2 * (2 + 1)  # bf16 rows in, e4m3 rows out
-    # a decode step of the same layer: 128 sequences, one token each
-    from pagedattn.metadata import decode_metadata
     lens = [int(x) for x in rng.integers(1, 8192, 128)]
     need = [(n + 15) // 16 for n in lens]
     perm = rng.permutation(sum(need))
@@ -354,86 +524,41 @@ def bench_kv_write(dev, steps: int = 20, warmup: int = 3) -> dict:
                            "GBps": fork_bytes / (fork_ms * 1e-3) / 1e9}}
 
 
-def cpu_decode_baseline(w, t, n_seq: int, kv_elem: int):
-    """fp32 oracle decode over the first n_seq sequences, timed on the host."""
-    import numpy as np
-    import torch
-
-    import oracle as O
-
-    cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
-    rows = list(range(min(n_seq, w.meta.batch_size)))
-    m = w.meta
-    # compact pool of the sampled sequences, copied to host once (untimed)
-    parts = [m.kv_indices[m.kv_indptr[b]:m.kv_indptr[b + 1]] for b in rows]
-    pages = np.concatenate(parts)
-    indptr = np.concatenate([[0], np.cumsum([len(p) for p in parts])]).astype(np.int32)
-    idx = torch.from_numpy(pages.astype(np.int64)).to(t.pool.device)
-    sub = t.pool.index_select(0, idx).cpu()
-    scales = None if t.scales is None else t.scales.index_select(0, idx).cpu()
-    q = t.q[rows].float().cpu()
-    ind = np.arange(len(pages), dtype=np.int32)
-    last = m.kv_last_page_len[rows]
-    # repeat the sample until about 10 s of CPU work has been timed
-    reps, elapsed = 0, 0.0
-    while elapsed < 10.0 or reps < 3:
-        t0 = time.perf_counter()
-        O.decode(q, sub, indptr, ind, last, scales=scales)
-        elapsed += time.perf_counter() - t0
-        reps += 1
-    sec = elapsed / reps
-    kv_bytes = int(m.seq_lens[rows].astype(np.int64).sum()) * w.hkv * w.d * 2 * kv_elem
-    byts = kv_bytes + len(rows) * w.hq * w.d * 4
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")),
-                         "unknown")
-    except OSError:
-        model = "unknown"
-    return {
-        "value": byts / sec / 1e9,
-        "unit": "GB/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": (f"{len(rows)} of {w.meta.batch_size} sequences of {w.name} "
-                   f"({int(m.seq_lens[rows].sum())} kv tokens), fp32 torch oracle, "
-                   f"{reps} passes in {elapsed:.1f} s ({sec:.3f} s each) on {model}"),
-    }
-
-
-def copy_calibration(dev, nbytes: int = 1 << 30, reps: int = 3) -> dict:
-    """A plain copy of known size: the reference point for HBM byte counters."""
+def calibration(dev, nbytes: int = 1 << 30, reps: int = 3) -> dict:
+    """A plain copy and a plain read of known size: the reference points for
+    the HBM byte counters (FETCH_SIZE / WRITE_SIZE)."""
     import torch
 
     import pagedattn
 
     src = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
-    for _ in range(reps):
-        pagedattn.copy_bytes(dst, src)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    pagedattn.copy_bytes(dst, src)
-    b.record()
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b)
-    return {"bytes_read": nbytes, "bytes_written": nbytes, "ms": ms,
-            "GBps": 2 * nbytes / (ms * 1e-3) / 1e9}
+    copy_ms = statistics.median(time_steps(lambda i: pagedattn.copy_bytes(dst, src), reps + 2, 1))
+    read_ms = statistics.median(time_steps(lambda i: pagedattn.read_bytes(src), reps + 2, 1))
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"copy": {"bytes_read": nbytes, "bytes_written": nbytes, "ms": copy_ms,
+                     "GBps": 2 * nbytes / (copy_ms * 1e-3) / 1e9},
+            "read": {"bytes_read": nbytes, "ms": read_ms,
+                     "GBps": nbytes / (read_ms * 1e-3) / 1e9}}
 
 
-def load_traffic() -> dict | None:
-    """HBM bytes per decode step measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
-    runs of this bench (scaled by the plain-copy calibration), as committed in
-    profiles/; None when absent."""
-    path = os.path.join(ROOT, "profiles", "decode_tinyllama_b256_hbm_traffic.json")
-    try:
-        with open(path) as f:
-            d = json.load(f)
-    except (OSError, ValueError):
-        return None
-    d["source"] = os.path.relpath(path, ROOT)
-    return d
+# -----------------------------------------------------------------------------
+
+DECODE_KERNEL = {
+    "c2": "decode step: decode_kernel<64, bf16, append> (each sequence's new K/V written, "
+          "then attention) + decode_merge_kernel (split-KV merge)",
+    "c4": "decode step: decode_kernel<128, bf16, append>, fixed 4096-token split-KV chunks "
+          "+ decode_merge_kernel",
+    "c4b": "decode step: decode_kernel<128, bf16, append>, planner's balanced split "
+           "+ decode_merge_kernel",
+    "c5d": "decode step: decode_kernel<128, e4m3 pool, append> + decode_merge_kernel",
+}
+PREFILL_KERNEL = {
+    "c3": "prefill_kernel<128, bf16> (causal, ragged, paged; bf16 MFMA)",
+    "c5p": "prefill_kernel<128, e4m3 pool> (K/V converted to bf16 in LDS; bf16 MFMA, priced "
+           "against the bf16 peak)",
+}
 
 
 def main() -> int:
@@ -442,14 +567,16 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--no-extra", action="store_true",
-                    help="skip the other workloads (long-context decode, ...)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--config", default="all",
+                    help="comma-separated subset of " + ",".join(CONFIGS) + " (default all)")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline (c2)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported",
               file=sys.stderr)
         return 2
+    args.steps = max(args.steps, 1)
     import torch
 
     from pagedattn import workloads as W
@@ -460,64 +587,81 @@ def main() -> int:
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     dtype = torch.bfloat16
+    want = set(CONFIGS) if args.config == "all" else set(args.config.split(","))
+    if args.no_extra:
+        want = {"c2"}
+    unknown = want - set(CONFIGS)
+    if unknown:
+        print(f"bench.py: unknown config(s) {sorted(unknown)}", file=sys.stderr)
+        return 2
+    cpu = not args.no_cpu
+    extra: dict = {}
+    steps_n = max(20, args.steps)  # >= 20 timed iterations per configuration
 
+    r = None
     main_w = W.tinyllama_decode(seed=args.seed)
-    r = bench_decode(main_w, args, dev, dtype, "tinyllama_decode",
-                     cpu_sample=0 if args.no_cpu else 256)
-    log(f"tinyllama_decode: step {r['ms_per_step']:.4f} ms, attention {r['attn_ms_avg']:.4f} ms "
-        f"= {r['attn_GBps']:.0f} GB/s ({100 * r['attn_frac']:.1f}% of 8 TB/s)")
-    extra = {}
-    if not args.no_extra:
-        lw = W.llama3_8b_long_decode(seed=args.seed)
-        lr = bench_decode(lw, argparse.Namespace(steps=max(5, args.steps // 3),
-                                                 warmup=2), dev, dtype,
-                          "llama3_8b_long_decode")
-        log(f"llama3_8b_long_decode: attention {lr['attn_ms_avg']:.3f} ms = "
-            f"{lr['attn_GBps']:.0f} GB/s ({100 * lr['attn_frac']:.1f}%)")
-        extra["llama3_8b_long_decode"] = {k: lr[k] for k in (
-            "ms_per_step", "attn_ms_avg", "attn_GBps", "attn_frac", "alg_bytes_attn",
-            "split_pages", "batch", "kv_tokens")}
-        # the planner's own balanced partition of the same batch
-        lb = bench_decode(dataclasses.replace(lw, split_pages=0),
-                          argparse.Namespace(steps=max(5, args.steps // 3), warmup=2), dev,
-                          dtype, "llama3_8b_long_decode.balanced")
-        log(f"llama3_8b_long_decode (balanced split): {lb['attn_GBps']:.0f} GB/s "
-            f"({100 * lb['attn_frac']:.1f}%)")
-        extra["llama3_8b_long_decode.balanced"] = {k: lb[k] for k in (
-            "ms_per_step", "attn_GBps", "attn_frac", "split_pages")}
-        pa_ = argparse.Namespace(steps=max(5, args.steps // 2), warmup=2)
-        pr = bench_prefill(W.llama3_8b_prefill(seed=args.seed), pa_, dev, dtype,
-                           "llama3_8b_prefill")
-        log(f"llama3_8b_prefill: attention {pr['attn_ms_avg']:.4f} ms = "
-            f"{pr['attn_TFLOPs']:.1f} TFLOP/s ({100 * pr['attn_frac']:.1f}% of bf16 peak)")
+    if "c2" in want:
+        r = bench_decode(main_w, args, dev, dtype, "tinyllama_decode",
+                         list(range(main_w.meta.batch_size)) if cpu else None, DECODE_KERNEL["c2"])
+        log(f"tinyllama_decode: step {r['ms_median'] * 1e3:.1f} us (median) = "
+            f"{r['step_GBps']:.0f} GB/s ({100 * r['frac']:.1f}% of 8 TB/s)")
+    sub = argparse.Namespace(steps=steps_n, warmup=3)
+    if "c3" in want:
+        pw = W.llama3_8b_prefill(seed=args.seed)
+        pr = bench_prefill(pw, sub, dev, dtype, "llama3_8b_prefill",
+                           list(range(pw.meta.batch_size)) if cpu else None, PREFILL_KERNEL["c3"])
+        log(f"llama3_8b_prefill: {pr['ms_median'] * 1e3:.1f} us = {pr['attn_TFLOPs']:.1f} "
+            f"TFLOP/s ({100 * pr['frac']:.1f}% of bf16 peak)")
         extra["llama3_8b_prefill"] = pr
+    if "c4" in want or "c4b" in want:
+        lw = W.llama3_8b_long_decode(seed=args.seed)
+        if "c4" in want:
+            lr = bench_decode(lw, sub, dev, dtype, "llama3_8b_long_decode",
+                              [0] if cpu else None, DECODE_KERNEL["c4"])
+            log(f"llama3_8b_long_decode: {lr['ms_median'] * 1e3:.0f} us = {lr['step_GBps']:.0f} "
+                f"GB/s ({100 * lr['frac']:.1f}%)")
+            extra["llama3_8b_long_decode"] = lr
+        if "c4b" in want:
+            lb = bench_decode(dataclasses.replace(lw, split_pages=0), sub, dev, dtype,
+                              "llama3_8b_long_decode.balanced", None, DECODE_KERNEL["c4b"])
+            log(f"llama3_8b_long_decode (balanced split): {lb['step_GBps']:.0f} GB/s "
+                f"({100 * lb['frac']:.1f}%)")
+            extra["llama3_8b_long_decode.balanced"] = lb
+    if "c5d" in want or "c5p" in want:
         dec5, pre5 = W.llama3_70b_mixed_fp8(seed=args.seed)
-        d5 = bench_decode(dec5, pa_, dev, dtype, "llama3_70b_mixed_fp8.decode")
-        p5 = bench_prefill(pre5, pa_, dev, dtype, "llama3_70b_mixed_fp8.prefill")
-        log(f"llama3_70b_mixed_fp8: decode {d5['attn_GBps']:.0f} GB/s "
-            f"({100 * d5['attn_frac']:.1f}%), prefill {p5['attn_TFLOPs']:.1f} TFLOP/s "
-            f"({100 * p5['attn_frac']:.1f}% of bf16 peak)")
-        extra["llama3_70b_mixed_fp8"] = {
-            "decode": {k: d5[k] for k in ("attn_ms_avg", "attn_GBps", "attn_frac",
-                                          "alg_bytes_attn", "batch", "kv_tokens")},
-            "prefill": p5,
-        }
+        c5 = {}
+        if "c5d" in want:
+            rng = __import__("numpy").random.default_rng(5)
+            rows = sorted(rng.choice(dec5.meta.batch_size, 8, replace=False).tolist())
+            d5 = bench_decode(dec5, sub, dev, dtype, "llama3_70b_mixed_fp8.decode",
+                              rows if cpu else None, DECODE_KERNEL["c5d"])
+            log(f"llama3_70b_mixed_fp8 decode: {d5['step_GBps']:.0f} GB/s "
+                f"({100 * d5['frac']:.1f}%)")
+            c5["decode"] = d5
+        if "c5p" in want:
+            p5 = bench_prefill(pre5, sub, dev, dtype, "llama3_70b_mixed_fp8.prefill",
+                               [0] if cpu else None, PREFILL_KERNEL["c5p"])
+            log(f"llama3_70b_mixed_fp8 prefill: {p5['attn_TFLOPs']:.1f} TFLOP/s "
+                f"({100 * p5['frac']:.1f}% of bf16 peak)")
+            c5["prefill"] = p5
+        extra["llama3_70b_mixed_fp8"] = c5
+    if "devplan" in want:
         dp = bench_device_plan(main_w, dev, dtype)
-        log(f"tinyllama_decode (device plan): eager {dp['eager_ms_per_step']:.4f} ms, "
-            f"HIP graph {dp['graph_ms_per_step']:.4f} ms per step "
-            f"({dp['graph_steps_per_graph']} steps per graph; "
-            f"{dp['graph_one_step_ms']:.4f} ms with one step per graph); metadata build "
-            f"{1e3 * dp['metadata_build_ms']:.1f} us")
+        log(f"tinyllama_decode (device plan): eager {dp['eager_ms_per_step'] * 1e3:.1f} us, "
+            f"HIP graph {dp['graph_ms_per_step'] * 1e3:.1f} us per step")
         extra["tinyllama_decode.device_plan"] = dp
+    if "kvwrite" in want:
         kw = bench_kv_write(dev)
         log(f"kv write path: e4m3 running-amax append {kw['append_e4m3_amax']['GBps']:.0f} GB/s "
-            f"(4096-token chunk), {1e3 * kw['append_e4m3_amax.decode']['ms']:.1f} us per "
-            f"128-token decode step; CoW fork {kw['fork_pages']['GBps']:.0f} GB/s")
+            f"(4096-token chunk); CoW fork {kw['fork_pages']['GBps']:.0f} GB/s")
         extra["kv_write"] = kw
-    cal = copy_calibration(dev)
-    traffic = load_traffic()
-    log(f"copy calibration: {cal['GBps']:.0f} GB/s (read+write)")
+    cal = calibration(dev)
+    log(f"calibration: copy {cal['copy']['GBps']:.0f} GB/s, read {cal['read']['GBps']:.0f} GB/s")
 
+    if r is None:  # a profiling subset without the headline
+        print(json.dumps({"config_subset": sorted(want), "extra": extra, "calibration": cal}),
+              flush=True)
+        return 0
     line = {
         "metric": "paged decode attn HBM GB/s (% of 8 TB/s); prefill attn TFLOP/s (% MFMA peak)",
         "value": round(r["step_GBps"], 2),
@@ -525,7 +669,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(r["ms_per_step"], 5),
+        "ms_per_step": round(r["ms_median"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -539,23 +683,14 @@ def main() -> int:
             "page_size": 16,
             "parallelism": "single GPU",
             "seed": args.seed,
+            "timing": "per-step HIP events on the launch stream; ms_per_step is the median",
         },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "decode step launch: decode_kernel<64, bf16, append> (new token's K/V "
-                      "written, then attention) plus its split-KV merge launch",
-            "achieved": round(r["step_GBps"], 2),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(r["step_GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": traffic.get("traffic_bytes_per_step") if traffic else None,
-            "traffic_source": traffic.get("source") if traffic else None,
-            "alg_bytes_per_launch": r["alg_bytes_step"],
-            "avg_launch_ms": round(r["ms_per_step"], 5),
-        },
-        "cpu_baseline": r.get("cpu"),
+        "roofline": r["roofline"],
+        "cpu_baseline": r.get("cpu_baseline"),
+        "step_stats_ms": {k: r[k] for k in ("ms_median", "ms_mean", "ms_min", "ms_max",
+                                            "iterations")},
         "extra": extra,
-        "copy_calibration": cal,
+        "calibration": cal,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -401,6 +401,13 @@ int pagedattn_decode_run_noalloc(int32_t batch_size, int32_t num_qo_heads,
 int pagedattn_copy_bytes(void* dst, const void* src, size_t bytes,
                          void* stream);
 
+/* No counterpart in the reference: a plain streaming read of `bytes` bytes
+ * (multiple of 16, 16-byte aligned), XOR-reduced into one dword per
+ * workgroup in sink[0, min(sink_entries, 8 x CUs)); the read-only point of
+ * the HBM byte-counter calibration. */
+int pagedattn_read_bytes(const void* src, size_t bytes, uint32_t* sink,
+                         int32_t sink_entries, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -237,6 +237,30 @@ __global__ void __launch_bounds__(256)
     dst[i] = src[i];
 }
 
+// plain streaming read, grid-stride, 16 bytes per thread and step: each
+// workgroup XOR-reduces what it read and writes one dword to sink[blockIdx],
+// so the kernel's HBM traffic is the read plus a few KiB of writes
+__global__ void __launch_bounds__(256)
+    read_kernel(const u32x4* __restrict__ src, int64_t n16, uint32_t* __restrict__ sink) {
+  __shared__ uint32_t red[256 / kWave];
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  uint32_t x = 0;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride) {
+    const u32x4 v = src[i];
+    x ^= v[0] ^ v[1] ^ v[2] ^ v[3];
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x ^= __shfl_xor(x, off);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int w = 0; w < 256 / kWave; ++w) r ^= red[w];
+    sink[blockIdx.x] = r;
+  }
+}
+
 }  // namespace pa
 
 using namespace pa;
@@ -505,6 +529,25 @@ int pagedattn_quantize_pages_e4m3(const void* src_cache, int32_t src_dtype,
                        (const uint16_t*)src_cache, (uint8_t*)dst_cache, scales,
                        block_elems);
   return check_launch("quantize_pages_e4m3");
+}
+
+int pagedattn_read_bytes(const void* src, size_t bytes, uint32_t* sink,
+                         int32_t sink_entries, void* stream) {
+  if ((bytes & 15) || !aligned16(src))
+    return set_error(PAGEDATTN_ERR_INVALID,
+                     "read_bytes: size and pointer must be 16-byte aligned");
+  if (bytes == 0) return PAGEDATTN_OK;
+  if (!sink || sink_entries <= 0)
+    return set_error(PAGEDATTN_ERR_INVALID, "read_bytes: null or empty sink");
+  const int64_t n16 = (int64_t)(bytes / 16);
+  int cus = device_cu_count();
+  if (cus <= 0) cus = 256;
+  int64_t blocks = (n16 + 255) / 256;
+  if (blocks > (int64_t)cus * 8) blocks = (int64_t)cus * 8;
+  if (blocks > sink_entries) blocks = sink_entries;
+  hipLaunchKernelGGL(read_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                     (const u32x4*)src, n16, sink);
+  return check_launch("read_bytes");
 }
 
 int pagedattn_copy_bytes(void* dst, const void* src, size_t bytes,

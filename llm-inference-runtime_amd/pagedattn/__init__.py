@@ -18,6 +18,7 @@ from .ops import (  # noqa: F401
     fork_pages,
     get_batch_indices_positions,
     quantize_pages_e4m3,
+    read_bytes,
     rope_append_paged_kv_cache,
 )
 from ._lib import LIB_PATH, PagedAttnError, lib  # noqa: F401
@@ -34,6 +35,7 @@ __all__ = [
     "fork_pages",
     "get_batch_indices_positions",
     "quantize_pages_e4m3",
+    "read_bytes",
     "rope_append_paged_kv_cache",
     "LIB_PATH",
     "PagedAttnError",

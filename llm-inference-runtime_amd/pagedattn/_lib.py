@@ -106,6 +106,7 @@ _SIGNATURES = {
     "pagedattn_quantize_pages_e4m3": (
         _c_int, [_c_p, _c_int, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_p]),
     "pagedattn_copy_bytes": (_c_int, [_c_p, _c_p, _c_sz, _c_p]),
+    "pagedattn_read_bytes": (_c_int, [_c_p, _c_sz, _c_p, _c_int, _c_p]),
     "pagedattn_decode_run_noalloc": (
         _c_int,
         [_c_int, _c_int, _c_int, _c_int, _c_int, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_int,

@@ -451,6 +451,16 @@ def copy_bytes(dst: torch.Tensor, src: torch.Tensor) -> None:
     call("pagedattn_copy_bytes", ptr(dst), ptr(src), n, _stream(src.device))
 
 
+def read_bytes(src: torch.Tensor) -> torch.Tensor:
+    """Plain streaming read of src (HBM counter calibration, read-only point);
+    returns the per-workgroup XOR of what was read."""
+    n = src.numel() * src.element_size()
+    sink = torch.empty(8 * max(1, _lib.lib().pagedattn_device_cu_count()), dtype=torch.int32,
+                       device=src.device)
+    call("pagedattn_read_bytes", ptr(src), n, ptr(sink), sink.numel(), _stream(src.device))
+    return sink
+
+
 # -----------------------------------------------------------------------------
 class _Plan:
     """Owns one host plan object of the library."""
