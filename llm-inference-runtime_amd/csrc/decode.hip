@@ -316,22 +316,14 @@ struct SoftmaxState {
   float m, l;
 };
 
-// The new-token row of the fused append lives in the wave's own LDS slot as
-// the bits stored in the pool (e4m3 pools: quantised with the page's scale):
-// K row at byte 0, V row at byte D * ESZ.  Only the pair holding the new
-// token reads it, so it costs no registers in the main loop.
 // One call handles NPC page pairs (one register stage) as one online-softmax
 // step: one cross-lane max and one rescale check for all of them, and their
-// independent MFMA chains interleave.  patch_k >= 0: page half patch_pi of
-// pair patch_k holds the token appended in this launch at `slot`; its stale
-// loaded values are replaced by the new row where they are used.
+// independent MFMA chains interleave.
 template <int D, bool BF16, bool FP8, int NPC>
 __device__ __forceinline__ void compute_pairs(const Stage<D, BF16, FP8> (&st)[NPC],
                                               const u32x4 (&qf)[D / 32],
                                               SoftmaxState<D, BF16, FP8>& sm,
-                                              float scale_log2, int G, int n,
-                                              const uint8_t* new_row, int patch_k,
-                                              int patch_pi, int slot) {
+                                              float scale_log2, int G, int n) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
   constexpr int NS = NPC * 8;  // scores per lane
@@ -344,12 +336,7 @@ __device__ __forceinline__ void compute_pairs(const Stage<D, BF16, FP8> (&st)[NP
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < Tr::KS; ++ks) {
-        typename Tr::KRaw kr = st[k].k[pi][ks];
-        if (patch_k == k && patch_pi == pi) {
-          const auto nk = *reinterpret_cast<const typename Tr::KRaw*>(
-              new_row + (32 * ks + 8 * G) * Tr::ESZ);
-          if (n == slot) kr = nk;
-        }
+        const typename Tr::KRaw kr = st[k].k[pi][ks];
         u32x4 a;
         if constexpr (FP8) {
           a = e4m3x8_to_16<BF16>(kr[0], kr[1]);
@@ -421,12 +408,7 @@ __device__ __forceinline__ void compute_pairs(const Stage<D, BF16, FP8> (&st)[NP
     uint32_t vw[8][VWORDS];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      typename Tr::VRaw vr = st[k].v[j];
-      if (patch_k == k && patch_pi == (j >> 2)) {
-        const auto nv = *reinterpret_cast<const typename Tr::VRaw*>(
-            new_row + (D + W * n) * Tr::ESZ);
-        if (G == (slot >> 2) && (j & 3) == (slot & 3)) vr = nv;
-      }
+      const typename Tr::VRaw vr = st[k].v[j];
 #pragma unroll
       for (int w = 0; w < VWORDS; ++w) vw[j][w] = dword_of(vr, w);
     }
@@ -462,37 +444,34 @@ __device__ __forceinline__ void compute_pairs(const Stage<D, BF16, FP8> (&st)[NP
 }
 
 // Writes sequence b / head h's new row to slot `slot` of page `page` (the
-// append of flashinfer.append_paged_kv_cache at position kv_len - 1) and to
-// the wave's LDS slot `new_row`.  Lanes [0, D/8) move the K row, lanes
-// [32, 32 + D/8) the V row, 8 elements each.
+// append of flashinfer.append_paged_kv_cache at position kv_len - 1).  Lanes
+// [0, D/8) move the K row, lanes [32, 32 + D/8) the V row, 8 elements each.
+// The same wave reads the page back later in program order (its own store
+// to the same addresses comes first), so the attention sees the new row
+// exactly as the pool holds it, with no patching of loaded registers.
 // With ROPE the K row is rotated first (position `pos`): lane c < D/16 takes
 // the chunk pair c, c + D/16 (elements i and i + D/2).
 template <int D, bool BF16, bool FP8>
-__device__ __forceinline__ void put_chunk(const DecodeParams& p, uint8_t* new_row,
-                                          int h, int page, int slot, int is_v, int c,
-                                          u32x4 x) {
+__device__ __forceinline__ void put_chunk(const DecodeParams& p, int h, int page, int slot,
+                                          int is_v, int c, u32x4 x) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   uint8_t* dst = const_cast<uint8_t*>(p.cache) +
                  (((int64_t)page * 2 + is_v) * p.hkv + h) * (int64_t)Tr::PAGE_BYTES +
                  ((int64_t)slot * D + 8 * c) * Tr::ESZ;
-  uint8_t* lds = new_row + (is_v * D + 8 * c) * Tr::ESZ;
   if constexpr (FP8) {
     const float scale =
         load_invariant(p.kv_scales + ((int64_t)page * 2 + is_v) * p.hkv + h);
     bool clamped = false;
     const u32x2 q = quant8_e4m3<BF16>(x, scale, &clamped);
     *reinterpret_cast<u32x2*>(dst) = q;
-    *reinterpret_cast<u32x2*>(lds) = q;
     count_lanes(p.append_err, clamped);
   } else {
     *reinterpret_cast<u32x4*>(dst) = x;
-    *reinterpret_cast<u32x4*>(lds) = x;
   }
 }
 
 template <int D, bool BF16, bool FP8, bool ROPE>
-__device__ __forceinline__ void fused_append(const DecodeParams& p,
-                                             uint8_t* new_row, int b, int h,
+__device__ __forceinline__ void fused_append(const DecodeParams& p, int b, int h,
                                              int page, int slot, int lane, int pos) {
   const int is_v = lane >> 5;
   const int c = lane & 31;
@@ -509,11 +488,11 @@ __device__ __forceinline__ void fused_append(const DecodeParams& p,
     for (int e = 0; e < 8; ++e)
       rope_cos_sin(pos, 8 * c + e, D, p.rope_inv_scale, p.rope_log2_theta, &cs[e], &sn[e]);
     rope8<BF16>(lo, hi, cs, sn);
-    put_chunk<D, BF16, FP8>(p, new_row, h, page, slot, 0, c, lo);
-    put_chunk<D, BF16, FP8>(p, new_row, h, page, slot, 0, c + D / 16, hi);
+    put_chunk<D, BF16, FP8>(p, h, page, slot, 0, c, lo);
+    put_chunk<D, BF16, FP8>(p, h, page, slot, 0, c + D / 16, hi);
     return;
   }
-  put_chunk<D, BF16, FP8>(p, new_row, h, page, slot, is_v, c,
+  put_chunk<D, BF16, FP8>(p, h, page, slot, is_v, c,
                           *reinterpret_cast<const u32x4*>(src + 8 * c));
 }
 
@@ -521,13 +500,10 @@ template <int D, bool BF16, bool FP8, bool APPEND, bool ROPE, bool IMPLICIT>
 __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
-  __shared__ __attribute__((aligned(16)))
-  uint8_t sm_new[4][APPEND ? 2 * D * DecodeTraits<D, BF16, FP8>::ESZ : 16];
   const int lane = threadIdx.x & 63;
   // wave-uniform by construction; readfirstlane tells the compiler, so item
   // fields are scalar loads and buffer descriptors stay in SGPRs
   const int wave = uniform(threadIdx.x >> 6);
-  uint8_t* new_row = sm_new[wave];
   // head group gw = the hg consecutive waves of a workgroup; wave wi of the
   // group takes KV head h0 + wi of every item, so the group reads each page's
   // K (then V) blocks of hg heads, one contiguous run, at the same time
@@ -585,7 +561,6 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
     // the item that holds the new token's page also performs the append (a
     // position outside the sequence's pages is skipped, as the stand-alone
     // append skips it)
-    int new_pg = -1;  // page index (within the sequence) of the new token
     const int new_slot = new_pos & (kPage - 1);
     if constexpr (APPEND) {
       const int pg = new_pos >= 0 ? new_pos / kPage : -1;
@@ -594,9 +569,7 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
         if (pg >= page_lo && pg < page_hi) {
           const int page = page_id(p, ind_lo, pg, npages);
           if (page >= 0) {
-            new_pg = pg;
-            fused_append<D, BF16, FP8, ROPE>(p, new_row, b, h, page, new_slot, lane,
-                                             new_pos);
+            fused_append<D, BF16, FP8, ROPE>(p, b, h, page, new_slot, lane, new_pos);
           } else {
             skipped = true;
           }
@@ -633,16 +606,7 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
     // pairs past the end of the item were loaded as empty pages (no tokens,
     // zero data) and add nothing
     auto compute_chunk = [&](Stage<D, BF16, FP8> (&st)[NP], int c) {
-      int patch_k = -1, patch_pi = -1;
-      if constexpr (APPEND) {
-        const int d_pg = new_pg - (page_lo + 2 * NP * c);
-        if (new_pg >= 0 && d_pg >= 0 && d_pg < 2 * NP) {
-          patch_k = d_pg >> 1;
-          patch_pi = d_pg & 1;
-        }
-      }
-      compute_pairs<D, BF16, FP8, NP>(st, qf, sm, p.scale_log2, G, n, new_row, patch_k,
-                                      patch_pi, new_slot);
+      compute_pairs<D, BF16, FP8, NP>(st, qf, sm, p.scale_log2, G, n);
     };
     if (n_chunks > 0) {
       Stage<D, BF16, FP8> sa[NP], sb[NP];
