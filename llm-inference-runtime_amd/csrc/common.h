@@ -50,8 +50,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base,
                                            (int)bytes, kRsrcWord3);
 }
 
-// Cache policy of buffer loads: kCachePolicyStream marks data read once
-// (K/V pages of a decode pass) as non-temporal.
+// Cache policy of buffer loads: kCachePolicyStream marks data read once as
+// non-temporal (the 16-bit K/V pages of a decode pass; each kernel picks the
+// policy it measured faster).
 constexpr int kCachePolicyDefault = 0;
 constexpr int kCachePolicyStream = 2;
 

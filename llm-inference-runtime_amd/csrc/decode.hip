@@ -81,34 +81,30 @@ struct DecodeParams {
   int32_t* append_err;
 };
 
-#ifndef DECODE_KV_POLICY
-#define DECODE_KV_POLICY kCachePolicyStream
-#endif
-
 template <int N>
 struct RawT;
 template <>
 struct RawT<16> {
   using type = u32x4;
-  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r,
-                                              uint32_t off) {
-    return buf_load16<DECODE_KV_POLICY>(r, off);
+  template <int POLICY>
+  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return buf_load16<POLICY>(r, off);
   }
 };
 template <>
 struct RawT<8> {
   using type = u32x2;
-  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r,
-                                              uint32_t off) {
-    return buf_load8<DECODE_KV_POLICY>(r, off);
+  template <int POLICY>
+  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return buf_load8<POLICY>(r, off);
   }
 };
 template <>
 struct RawT<4> {
   using type = uint32_t;
-  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r,
-                                              uint32_t off) {
-    return buf_load4<DECODE_KV_POLICY>(r, off);
+  template <int POLICY>
+  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return buf_load4<POLICY>(r, off);
   }
 };
 
@@ -189,6 +185,13 @@ struct DecodeTraits {
       (FP8 && D == 128) ? 1 : ((kPage * D * ESZ * 2 * 2 >= 16384) ? 1 : 2);
   using KRaw = typename RawT<KB>::type;
   using VRaw = typename RawT<VB>::type;
+  // Cache policy of the K/V loads.  16-bit pools stream (non-temporal); e4m3
+  // pools load with the default policy.  Measured on the decode steps, with
+  // pools rotated past the Infinity Cache: the 70B-shaped e4m3 batch takes
+  // 225 us with the default policy against 276 us streamed, while the bf16
+  // long-context and TinyLlama steps take 1946 / 66 us with it against
+  // 1799 / 58 us streamed.
+  static constexpr int KV_POLICY = FP8 ? kCachePolicyDefault : kCachePolicyStream;
 };
 
 template <int D, bool BF16, bool FP8>
@@ -294,11 +297,11 @@ __device__ __forceinline__ void load_pair(Stage<D, BF16, FP8>& st,
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, bytes);
 #pragma unroll
     for (int ks = 0; ks < Tr::KS; ++ks)
-      st.k[pi][ks] = RawT<Tr::KB>::load(
+      st.k[pi][ks] = RawT<Tr::KB>::template load<Tr::KV_POLICY>(
           rk, (uint32_t)((n * D + 32 * ks + 8 * G) * Tr::ESZ));
 #pragma unroll
     for (int r = 0; r < 4; ++r)
-      st.v[pi * 4 + r] = RawT<Tr::VB>::load(
+      st.v[pi * 4 + r] = RawT<Tr::VB>::template load<Tr::KV_POLICY>(
           rv, (uint32_t)(((4 * G + r) * D + Tr::W * n) * Tr::ESZ));
     if constexpr (FP8) {
       const int64_t si = ((int64_t)page * 2) * p.hkv + h;
