@@ -220,13 +220,16 @@ def bench_decode(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
             q_data_type=dtype, split_pages=w.split_pages)
     torch.cuda.synchronize()
     plan_ms = (time.perf_counter() - tp) * 1e3
+    kind = dw.plan_kind
+    if isinstance(kernel, dict):
+        kernel = kernel.get(kind, kernel["split"])
     outs = [torch.empty((w.meta.batch_size, w.hq, w.d), dtype=dtype, device=dev)
             for _ in range(reps)]
 
     def step(i):
         # the decode step: each sequence's new K/V appended at kv_len - 1,
         # then attention, in one launch (pagedattn_decode_run_append), plus
-        # the split-KV merge launch when the plan cut sequences
+        # the split-KV merge launch when a split plan cut sequences
         t = inst[i % reps]
         dw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps], append_key=t.k_new,
                append_value=t.v_new)
@@ -244,6 +247,7 @@ def bench_decode(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         "batch": w.meta.batch_size,
         "kv_tokens": int(w.meta.seq_lens.sum()),
         "split_pages": w.split_pages,
+        "plan_kind": kind,
     }
     res["frac"] = res["step_GBps"] / HBM_PEAK_GBS
     res["roofline"] = roofline("hbm", kernel, res["step_GBps"], alg_step, ms, label)
@@ -545,9 +549,14 @@ def calibration(dev, nbytes: int = 1 << 30, reps: int = 3) -> dict:
 
 # -----------------------------------------------------------------------------
 
+# decode kernels per plan kind ("split": head-group work list + merge launch;
+# "shared": whole (sequence, KV head) items per CU workgroup, one launch)
 DECODE_KERNEL = {
     "c2": "decode step: decode_kernel<64, bf16, append> (each sequence's new K/V written, "
           "then attention) + decode_merge_kernel (split-KV merge)",
+    "c2.shared": "decode step: decode_shared_kernel<64, bf16, append> (each sequence's new "
+                 "K/V written, then attention; whole (sequence, KV head) items shared by the "
+                 "four waves of one workgroup per CU, one launch)",
     "c4": "decode step: decode_kernel<128, bf16, append>, fixed 4096-token split-KV chunks "
           "+ decode_merge_kernel",
     "c4b": "decode step: decode_kernel<128, bf16, append>, planner's balanced split "
@@ -602,7 +611,8 @@ def main() -> int:
     main_w = W.tinyllama_decode(seed=args.seed)
     if "c2" in want:
         r = bench_decode(main_w, args, dev, dtype, "tinyllama_decode",
-                         list(range(main_w.meta.batch_size)) if cpu else None, DECODE_KERNEL["c2"])
+                         list(range(main_w.meta.batch_size)) if cpu else None,
+                         {"split": DECODE_KERNEL["c2"], "shared": DECODE_KERNEL["c2.shared"]})
         log(f"tinyllama_decode: step {r['ms_median'] * 1e3:.1f} us (median) = "
             f"{r['step_GBps']:.0f} GB/s ({100 * r['frac']:.1f}% of 8 TB/s)")
     sub = argparse.Namespace(steps=steps_n, warmup=3)

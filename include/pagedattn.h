@@ -267,6 +267,22 @@ int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
                                  int32_t head_dim, int32_t page_size, void* workspace,
                                  size_t workspace_bytes);
 
+/* Which partition a decode plan holds (a diagnostic with no counterpart in
+ * the reference, for tests and benchmarks): PAGEDATTN_DECODE_SPLIT (a work
+ * list of head groups; sequences cut between groups are merged by a second
+ * launch), PAGEDATTN_DECODE_SHARED (whole (sequence, KV head) items per
+ * CU-sized workgroup whose waves share each item's pages; one launch),
+ * PAGEDATTN_DECODE_DEVICE (partition made on the device at run time), or 0
+ * for a plan that is not a decode plan.  pagedattn_decode_plan with
+ * split_pages = 0 takes a shared plan at head_dim 64 when its busiest CU
+ * carries at most PAGEDATTN_DECODE_SHARED_SLACK_KB (environment, default 96)
+ * KiB more K/V than the mean; PAGEDATTN_DECODE_SHARED=0 / =1 turns that off
+ * / takes one whenever it fits. */
+#define PAGEDATTN_DECODE_SPLIT 1
+#define PAGEDATTN_DECODE_SHARED 2
+#define PAGEDATTN_DECODE_DEVICE 3
+int pagedattn_decode_plan_kind(const pagedattn_plan* plan);
+
 /* BatchDecodeWithPagedKVCacheWrapper.forward(q, paged_kv_cache)
  * (src/models/llama.py:230-245).  q [batch, num_qo_heads, head_dim] strided;
  * out [batch, num_qo_heads, head_dim] contiguous, q dtype; lse (optional,

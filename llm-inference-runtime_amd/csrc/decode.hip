@@ -499,6 +499,53 @@ __device__ __forceinline__ void fused_append(const DecodeParams& p, int b, int h
                           *reinterpret_cast<const u32x4*>(src + 8 * c));
 }
 
+// Final normalisation of one softmax state of (sequence b, KV head h): the
+// output rows (and lse) of its g query heads, or base-2 split partials at
+// `slot` when slot >= 0.  Lane (G, n) owns d = W (4 G + r) + e of head n.
+template <int D, bool BF16, bool FP8>
+__device__ __forceinline__ void write_item_output(const DecodeParams& p, int b, int h, int slot,
+                                                  const SoftmaxState<D, BF16, FP8>& sm, int G,
+                                                  int n) {
+  constexpr int W = DecodeTraits<D, BF16, FP8>::W;
+  const int g = p.g;
+  const float l_tot = sum_over_groups16(sm.l);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  const float lse2 = l_tot > 0.f ? sm.m + log2f(l_tot) : -INFINITY;
+  if (slot < 0) {
+    if (n < g) {
+      uint16_t* orow = p.out + ((int64_t)b * p.hq + h * g + n) * D;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        uint16_t* dst = orow + W * (4 * G + r);
+        if constexpr (W == 8) {
+          u32x4 w4;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            w4[i] = pack2<BF16>(sm.o[2 * i][r] * inv, sm.o[2 * i + 1][r] * inv);
+          *reinterpret_cast<u32x4*>(dst) = w4;
+        } else {
+          u32x2 w2;
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            w2[i] = pack2<BF16>(sm.o[2 * i][r] * inv, sm.o[2 * i + 1][r] * inv);
+          *reinterpret_cast<u32x2*>(dst) = w2;
+        }
+      }
+      if (p.lse && G == 0)
+        p.lse[(int64_t)b * p.hq + h * g + n] = lse2 * 0.69314718055994531f;
+    }
+  } else {
+    if (n < g) {
+      float* prow = p.partial_o + ((int64_t)slot * g + n) * D;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int e = 0; e < W; ++e) prow[W * (4 * G + r) + e] = sm.o[e][r] * inv;
+      if (G == 0) p.partial_lse[(int64_t)slot * g + n] = lse2;
+    }
+  }
+}
+
 template <int D, bool BF16, bool FP8, bool APPEND, bool ROPE, bool IMPLICIT>
 __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
   using Tr = DecodeTraits<D, BF16, FP8>;
@@ -628,44 +675,7 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
       }
     }
 
-    // ---- epilogue from registers: lane (G, n) owns d = W (4 G + r) + e of
-    // head n
-    const float l_tot = sum_over_groups16(sm.l);
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    const float lse2 = l_tot > 0.f ? sm.m + log2f(l_tot) : -INFINITY;
-    if (slot < 0) {
-      if (n < g) {
-        uint16_t* orow = p.out + ((int64_t)b * p.hq + h * g + n) * D;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          uint16_t* dst = orow + W * (4 * G + r);
-          if constexpr (W == 8) {
-            u32x4 w4;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-              w4[i] = pack2<BF16>(sm.o[2 * i][r] * inv, sm.o[2 * i + 1][r] * inv);
-            *reinterpret_cast<u32x4*>(dst) = w4;
-          } else {
-            u32x2 w2;
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-              w2[i] = pack2<BF16>(sm.o[2 * i][r] * inv, sm.o[2 * i + 1][r] * inv);
-            *reinterpret_cast<u32x2*>(dst) = w2;
-          }
-        }
-        if (p.lse && G == 0)
-          p.lse[(int64_t)b * p.hq + h * g + n] = lse2 * 0.69314718055994531f;
-      }
-    } else {
-      if (n < g) {
-        float* prow = p.partial_o + ((int64_t)slot * g + n) * D;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-#pragma unroll
-          for (int e = 0; e < W; ++e) prow[W * (4 * G + r) + e] = sm.o[e][r] * inv;
-        if (G == 0) p.partial_lse[(int64_t)slot * g + n] = lse2;
-      }
-    }
+    write_item_output<D, BF16, FP8>(p, b, h, slot, sm, G, n);
   };
 
   if constexpr (!IMPLICIT) {
@@ -729,6 +739,321 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
       ++hgrp;
     }
   }
+}
+
+// ----------------------------------------------------------------------------
+// Shared-item decode (plans of pagedattn_decode_plan whose whole (sequence,
+// KV head) items balance over the CUs).  Workgroup w holds one CU, one wave
+// per SIMD, and owns the items [wave_ptr[w], wave_ptr[w + 1]).  The chunks
+// of its items (NP page pairs each, items in list order) form one sequence
+// that the four waves take in turn (wave w: chunks w, w + 4, ...).  A wave
+// keeps one softmax state: when it reaches a chunk of a later item it leaves
+// its state for the earlier item in an LDS slot, and the wave that completes
+// the item's chunk count merges the states left there, in wave order, and
+// writes the output.  No sequence is
+// cut across workgroups, so there are no split partials and no merge launch.
+
+constexpr int kSharedMaxItems = 8;  // items per workgroup (the planner's bound)
+constexpr int kSharedSlots = 2;     // items whose states can wait in LDS at once
+// Bound of the wait for a slot to be released (each round sleeps ~64 clocks);
+// the wait always ends long before, since a slot only waits for items of
+// lower index, whose waves never wait for it.
+constexpr int kSharedSpinLimit = 1 << 24;
+
+struct SharedItem {
+  int32_t b, h, chunk_lo, n_chunks;
+};
+
+template <int D>
+struct SharedLds {
+  int total;      // chunks of the workgroup's items
+  int tag[kSharedSlots];   // item index the slot is open for
+  int cnt[kSharedSlots];   // chunks accounted for by the states left in the slot
+  int mask[kSharedSlots];  // waves whose states are in the slot
+  int b[kSharedMaxItems], h[kSharedMaxItems], chunk_lo[kSharedMaxItems],
+      n_chunks[kSharedMaxItems], ind_lo[kSharedMaxItems], npages[kSharedMaxItems],
+      last[kSharedMaxItems], new_pos[kSharedMaxItems];
+  u32x4 q[kSharedMaxItems][D / 32][kWave];  // Q B-operands (rotated with ROPE)
+  struct State {
+    f32x4 o[D / 16][kWave];
+    float m[kWave], l[kWave];
+  } st[kSharedSlots][4];
+};
+
+// A claimed chunk: item index in the workgroup's table (-1: none left) and
+// its first page within the sequence.
+struct ChunkRef {
+  int item, pg0;
+};
+
+template <int D, bool BF16, bool FP8, bool APPEND, bool ROPE>
+__global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
+  using Tr = DecodeTraits<D, BF16, FP8>;
+  constexpr int W = Tr::W;
+  constexpr int NP = Tr::NP;
+  __shared__ SharedLds<D> L;
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int n = lane & 15;
+  const int G = lane >> 4;
+  const int g = p.g;
+  const int it_lo = uniform(load_invariant(p.wave_ptr + blockIdx.x));
+  const int n_it = min(max(uniform(load_invariant(p.wave_ptr + blockIdx.x + 1)) - it_lo, 0),
+                       kSharedMaxItems);
+  if (n_it == 0) return;  // uniform over the workgroup: no barrier is skipped by part of it
+  const SharedItem* items = reinterpret_cast<const SharedItem*>(p.items) + it_lo;
+
+  // ---- item table: thread t < n_it fills item t from the plan and the
+  // metadata of this launch; an item that does not match the launch keeps
+  // its chunks but reads and writes nothing (b = -1, no pages)
+  {
+    const int t = threadIdx.x;
+    bool skipped = false;
+    if (t < n_it) {
+      const SharedItem it = items[t];
+      int b = it.b, h = it.h, ind_lo = 0, npages = 0, last = kPage, new_pos = -1;
+      if (b < 0 || b >= p.batch_size || h < 0 || h >= p.hkv) {
+        b = -1;
+      } else {
+        ind_lo = load_invariant(p.kv_indptr + b);
+        npages = max(0, load_invariant(p.kv_indptr + b + 1) - ind_lo);
+        last = min(max(load_invariant(p.last_page_len + b), 1), kPage);
+        new_pos = npages > 0 ? (npages - 1) * kPage + last - 1 : -1;
+        if (APPEND && p.new_pos) new_pos = load_invariant(p.new_pos + b);
+        // a new token outside the sequence's pages is skipped (counted once
+        // per sequence, by its KV head 0)
+        const int pg = new_pos >= 0 ? new_pos / kPage : -1;
+        skipped = APPEND && h == 0 && npages > 0 && !(pg >= 0 && pg < npages);
+      }
+      L.b[t] = b;
+      L.h[t] = h;
+      L.chunk_lo[t] = it.chunk_lo;
+      L.n_chunks[t] = max(it.n_chunks, 0);
+      L.ind_lo[t] = ind_lo;
+      L.npages[t] = npages;
+      L.last[t] = last;
+      L.new_pos[t] = new_pos;
+      if (t == n_it - 1) L.total = it.chunk_lo + max(it.n_chunks, 0);
+    }
+    if (t < kSharedSlots) {
+      L.tag[t] = t;
+      L.cnt[t] = 0;
+      L.mask[t] = 0;
+    }
+    if constexpr (APPEND) count_lanes(p.append_err, skipped);
+  }
+  __syncthreads();
+
+  // the table in lanes: lane i < n_it holds item i's fields
+  const int li = lane < n_it ? lane : 0;
+  const int t_b = L.b[li], t_h = L.h[li], t_lo = L.chunk_lo[li], t_nc = L.n_chunks[li],
+            t_ind = L.ind_lo[li], t_np = L.npages[li], t_last = L.last[li],
+            t_pos = L.new_pos[li];
+  const int total = uniform(L.total);
+  auto field = [](int v, int i) { return __builtin_amdgcn_readlane(v, i); };
+
+  // ---- Q of the wave's items (items wave and wave + 4), loaded before the
+  // first K/V loads so that waiting for them never waits for K/V
+  constexpr int QPW = kSharedMaxItems / 4;
+  u32x4 qtmp[QPW][D / 32];
+#pragma unroll
+  for (int k = 0; k < QPW; ++k) {
+    const int i = wave + 4 * k;
+    const int b = i < n_it ? field(t_b, i) : -1;
+    const int h = b >= 0 ? field(t_h, i) : 0;
+    // unconditional loads (a padded head reads head 0's row and is zeroed
+    // when the rows are stored), so no wait is placed right after them
+    const bool hv = b >= 0 && n < g;
+    const uint16_t* qrow =
+        p.q + (int64_t)(b < 0 ? 0 : b) * p.q_sn + (int64_t)(h * g + (hv ? n : 0)) * p.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks)
+      qtmp[k][ks] = *reinterpret_cast<const u32x4*>(qrow + 32 * ks + 8 * G);
+  }
+
+  // wave w takes chunks w, w + 4, w + 8, ... of the sequence: a fixed
+  // assignment, so the states merged per item (and the output bits) do not
+  // depend on timing
+  int next_chunk = wave;
+  auto claim = [&]() -> ChunkRef {
+    const int c = next_chunk;
+    next_chunk += 4;
+    if (c >= total) return ChunkRef{-1, 0};
+    const int cnt = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < n_it && t_lo <= c));
+    const int it = uniform(cnt > 0 ? cnt - 1 : 0);
+    return ChunkRef{it, (c - field(t_lo, it)) * 2 * NP};
+  };
+  // no chunk left: page ids -1, so the loads below read nothing
+  auto fetch = [&](PairIds (&ids)[NP], const ChunkRef& r) {
+    const int it = max(r.item, 0);
+    const int ind_lo = field(t_ind, it), np = r.item < 0 ? 0 : field(t_np, it);
+#pragma unroll
+    for (int k = 0; k < NP; ++k) ids[k] = fetch_ids(p, ind_lo, r.pg0 + 2 * k, np);
+  };
+  // loads are issued whether or not a chunk was claimed (an empty one reads
+  // nothing), so every iteration issues the same number and the compiler's
+  // wait for one stage never waits for the other
+  auto load = [&](Stage<D, BF16, FP8> (&st)[NP], const PairIds (&ids)[NP], const ChunkRef& r) {
+    const int it = max(r.item, 0);
+    const int h = r.item < 0 ? 0 : field(t_h, it), np = field(t_np, it), last = field(t_last, it);
+#pragma unroll
+    for (int k = 0; k < NP; ++k) load_pair(st[k], p, h, ids[k], r.pg0 + 2 * k, np, last, n, G);
+  };
+
+  // Q operands into LDS (rotated with ROPE); lanes of padded heads store zeros
+  auto store_q = [&]() {
+#pragma unroll
+    for (int k = 0; k < QPW; ++k) {
+      const int i = wave + 4 * k;
+      if (i < n_it) {
+        if constexpr (ROPE) {
+          const int rope_at = field(t_pos, i);
+#pragma unroll
+          for (int ks = 0; ks < D / 64; ++ks) {
+            float cs[8], sn[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              rope_cos_sin(rope_at, 32 * ks + 8 * G + e, D, p.rope_inv_scale,
+                           p.rope_log2_theta, &cs[e], &sn[e]);
+            rope8<BF16>(qtmp[k][ks], qtmp[k][ks + D / 64], cs, sn);
+          }
+        }
+        const bool hv = field(t_b, i) >= 0 && n < g;
+#pragma unroll
+        for (int ks = 0; ks < D / 32; ++ks) {
+          const u32x4 z = {0u, 0u, 0u, 0u};
+          L.q[i][ks][lane] = hv ? qtmp[k][ks] : z;
+        }
+      }
+    }
+  };
+
+  // ---- appends: the wave of item i writes its new K/V rows, waits for the
+  // stores, and the barrier orders them before every wave's first K/V load
+  // (any wave may load the page); without appends the first chunk's loads
+  // are issued before the barrier
+  if constexpr (APPEND) {
+#pragma unroll
+    for (int k = 0; k < QPW; ++k) {
+      const int i = wave + 4 * k;
+      if (i >= n_it) continue;
+      const int b = field(t_b, i), h = field(t_h, i), np = field(t_np, i), pos = field(t_pos, i);
+      const int pg = pos >= 0 ? pos / kPage : -1;
+      if (b < 0 || pg < 0 || pg >= np) continue;
+      const int page = page_id(p, field(t_ind, i), pg, np);
+      if (page >= 0)
+        fused_append<D, BF16, FP8, ROPE>(p, b, h, page, pos & (kPage - 1), lane, pos);
+      else
+        count_lanes(p.append_err, h == 0 && lane == 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the appended rows are in L2
+    store_q();
+    __syncthreads();
+  }
+
+  Stage<D, BF16, FP8> sa[NP], sb[NP];
+  PairIds ida[NP], idb[NP];
+  ChunkRef ra = claim();
+  fetch(ida, ra);
+  ChunkRef rb = claim();
+  fetch(idb, rb);
+  load(sa, ida, ra);
+  if constexpr (!APPEND) {
+    store_q();
+    __syncthreads();
+  }
+
+  SoftmaxState<D, BF16, FP8> sm;
+  u32x4 qf[D / 32];
+  int cur = -1, kcur = 0;
+
+  // leaves the state of item i in its slot; the wave that completes the
+  // item's chunk count merges every state there and writes the output
+  auto flush = [&](int i, int k) {
+    const int s = i % kSharedSlots;
+    for (int spin = 0;; ++spin) {
+      const int tg = uniform(__hip_atomic_load(&L.tag[s], __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP));
+      if (tg == i || spin >= kSharedSpinLimit) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    typename SharedLds<D>::State& mine = L.st[s][wave];
+#pragma unroll
+    for (int e = 0; e < W; ++e) mine.o[e][lane] = sm.o[e];
+    mine.m[lane] = sm.m;
+    mine.l[lane] = sm.l;
+    int old = 0;
+    if (lane == 0) {
+      __hip_atomic_fetch_or(&L.mask[s], 1 << wave, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+      old = __hip_atomic_fetch_add(&L.cnt[s], k, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    old = uniform(old);
+    if (old + k != field(t_nc, i)) return;
+    const int mask = uniform(__hip_atomic_load(&L.mask[s], __ATOMIC_ACQUIRE,
+                                               __HIP_MEMORY_SCOPE_WORKGROUP));
+    // every state in the slot (this wave's included), in wave order against
+    // their common max, so the sum does not depend on which wave came last
+    float M = -INFINITY;
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2)
+      if ((mask >> w2) & 1) M = fmaxf(M, L.st[s][w2].m[lane]);
+    sm.m = M;
+    sm.l = 0.f;
+#pragma unroll
+    for (int e = 0; e < W; ++e) sm.o[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int w2 = 0; w2 < 4; ++w2) {
+        if (!((mask >> w2) & 1)) continue;
+        const typename SharedLds<D>::State& o2 = L.st[s][w2];
+        const float m2 = o2.m[lane];
+        const float a2 = m2 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m2 - M);
+        sm.l += o2.l[lane] * a2;
+#pragma unroll
+        for (int e = 0; e < W; ++e) sm.o[e] += o2.o[e][lane] * a2;
+      }
+    }
+    const int b = field(t_b, i);
+    if (b >= 0) write_item_output<D, BF16, FP8>(p, b, field(t_h, i), -1, sm, G, n);
+    if (lane == 0) {
+      __hip_atomic_store(&L.cnt[s], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_store(&L.mask[s], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_store(&L.tag[s], i + kSharedSlots, __ATOMIC_RELEASE,
+                         __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+  };
+  auto compute = [&](Stage<D, BF16, FP8> (&st)[NP], const ChunkRef& r) {
+    if (r.item != cur) {
+      if (cur >= 0) flush(cur, kcur);
+      cur = r.item;
+      kcur = 0;
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks) qf[ks] = L.q[cur][ks][lane];
+#pragma unroll
+      for (int e = 0; e < W; ++e) sm.o[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+      sm.m = -INFINITY;
+      sm.l = 0.f;
+    }
+    compute_pairs<D, BF16, FP8, NP>(st, qf, sm, p.scale_log2, G, n);
+    ++kcur;
+  };
+
+  // ---- chunks: two register stages, the next chunk's loads in flight while
+  // the current one is computed, page ids one chunk further ahead
+  while (ra.item >= 0) {
+    ChunkRef rc = claim();
+    fetch(ida, rc);
+    load(sb, idb, rb);
+    compute(sa, ra);
+    if (rb.item < 0) break;
+    ChunkRef rd = claim();
+    fetch(idb, rd);
+    load(sa, ida, rc);
+    compute(sb, rb);
+    ra = rc;
+    rb = rd;
+  }
+  if (cur >= 0) flush(cur, kcur);
 }
 
 // Combine the base-2 partials of n pieces, slot_of(s) giving piece s's
@@ -871,6 +1196,26 @@ DecodeFn decode_fn_d(bool bf16, bool fp8, bool append, bool rope) {
              : decode_fn<D, false, false, IMPLICIT>(append, rope);
 }
 
+template <int D, bool BF16, bool FP8>
+DecodeFn decode_shared_fn(bool append, bool rope) {
+  if (!append) return decode_shared_kernel<D, BF16, FP8, false, false>;
+  return rope ? decode_shared_kernel<D, BF16, FP8, true, true>
+              : decode_shared_kernel<D, BF16, FP8, true, false>;
+}
+
+template <int D>
+DecodeFn decode_shared_fn_d(bool bf16, bool fp8, bool append, bool rope) {
+  if (bf16)
+    return fp8 ? decode_shared_fn<D, true, true>(append, rope)
+               : decode_shared_fn<D, true, false>(append, rope);
+  return fp8 ? decode_shared_fn<D, false, true>(append, rope)
+             : decode_shared_fn<D, false, false>(append, rope);
+}
+
+static DecodeFn pick_decode_shared(int d, bool bf16, bool fp8, bool append, bool rope) {
+  return d == 64 ? decode_shared_fn_d<64>(bf16, fp8, append, rope) : nullptr;
+}
+
 static DecodeFn pick_decode(int d, bool bf16, bool fp8, bool append, bool rope, bool implicit) {
   if (d == 64)
     return implicit ? decode_fn_d<64, true>(bf16, fp8, append, rope)
@@ -915,6 +1260,93 @@ static int decode_head_group(int hkv) {
   return hg;
 }
 
+// Shared-item plans (decode_shared_kernel): PAGEDATTN_DECODE_SHARED=0 turns
+// them off, =1 takes one whenever the items fit a workgroup's table; by
+// default one is taken when its busiest CU holds at most
+// PAGEDATTN_DECODE_SHARED_SLACK_KB KiB more K/V than the mean (default 96:
+// what one CU streams in about the 4-5 us that the split's merge launch
+// costs).
+static int decode_shared_mode() {
+  if (const char* env = std::getenv("PAGEDATTN_DECODE_SHARED")) {
+    const int v = std::atoi(env);
+    if (v == 0 || v == 1) return v;
+  }
+  return -1;
+}
+static int64_t decode_shared_slack_bytes() {
+  if (const char* env = std::getenv("PAGEDATTN_DECODE_SHARED_SLACK_KB")) {
+    const int v = std::atoi(env);
+    if (v >= 0) return (int64_t)v << 10;
+  }
+  return (int64_t)96 << 10;
+}
+
+// Page pairs per register stage of the decode kernels: DecodeTraits::NP,
+// which depends on D only (2 at D = 64, 1 at D = 128, for every pool dtype).
+static int decode_stage_pairs(int d) { return d == 64 ? 2 : 1; }
+static_assert(DecodeTraits<64, true, false>::NP == 2 && DecodeTraits<64, true, true>::NP == 2 &&
+                  DecodeTraits<128, true, false>::NP == 1 &&
+                  DecodeTraits<128, true, true>::NP == 1,
+              "decode_stage_pairs must mirror DecodeTraits::NP");
+
+// Shared-item partition: whole (sequence, KV head) items, longest first onto
+// the least-loaded of `cus` workgroups, in chunks of decode_stage_pairs page
+// pairs.  Returns false (and leaves the outputs unspecified) when some
+// workgroup would hold more than kSharedMaxItems items or, unless forced,
+// when the busiest workgroup exceeds the mean by more than the slack.
+static bool plan_shared(const std::vector<int32_t>& npages, int hkv, int d, int cus, bool forced,
+                        std::vector<SharedItem>* items, std::vector<int32_t>* wg_ptr) {
+  const int batch = (int)npages.size();
+  const int64_t n_all = (int64_t)batch * hkv;
+  // built for D = 64: at D = 128 two register stages, the merge and the
+  // output conversion do not fit the register file together
+  if (n_all == 0 || d != 64) return false;
+  const int chunk_pages = 2 * decode_stage_pairs(d);
+  std::vector<int32_t> order((size_t)n_all);
+  for (int64_t i = 0; i < n_all; ++i) order[(size_t)i] = (int32_t)i;
+  // sequence-major item ids; longest first, ties in id order
+  std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t c) {
+    return npages[a / hkv] > npages[c / hkv];
+  });
+  const int n_wg = (int)std::min<int64_t>(std::max(cus, 1), n_all);
+  std::vector<std::vector<int32_t>> per(n_wg);
+  std::vector<int64_t> load(n_wg, 0);
+  std::priority_queue<std::pair<int64_t, int>, std::vector<std::pair<int64_t, int>>,
+                      std::greater<std::pair<int64_t, int>>> heap;
+  for (int w = 0; w < n_wg; ++w) heap.push({0, w});
+  for (int32_t id : order) {
+    auto top = heap.top();
+    heap.pop();
+    per[top.second].push_back(id);
+    // a chunk streams its pages; an empty item still costs one chunk's visit
+    top.first += std::max(1, npages[id / hkv]);
+    load[top.second] = top.first;
+    heap.push(top);
+  }
+  int64_t sum = 0, mx = 0;
+  for (int w = 0; w < n_wg; ++w) {
+    if ((int)per[w].size() > kSharedMaxItems) return false;
+    sum += load[w];
+    mx = std::max(mx, load[w]);
+  }
+  // K and V of one page of one KV head, counted at 16 bits per element
+  const int64_t page_bytes = (int64_t)kPage * d * 2 * 2;
+  if (!forced && (mx * n_wg - sum) * page_bytes > decode_shared_slack_bytes() * n_wg) return false;
+  items->clear();
+  wg_ptr->assign(1, 0);
+  for (int w = 0; w < n_wg; ++w) {
+    int32_t chunk = 0;
+    for (int32_t id : per[w]) {
+      const int32_t np = npages[id / hkv];
+      const int32_t nc = std::max<int32_t>(1, ((np + 1) / 2 + chunk_pages / 2 - 1) / (chunk_pages / 2));
+      items->push_back(SharedItem{id / hkv, id % hkv, chunk, nc});
+      chunk += nc;
+    }
+    wg_ptr->push_back((int32_t)items->size());
+  }
+  return true;
+}
+
 // The device-side partition of a decode plan (pagedattn_decode_plan_device
 // and pagedattn_decode_run_noalloc): shares of the (sequence, head group,
 // page) stream for cus x waves-per-CU / hg head groups, split partials at
@@ -937,6 +1369,7 @@ static int setup_device_plan(const char* who, pagedattn_plan* plan, int32_t batc
     return set_error(PAGEDATTN_ERR_WORKSPACE, "%s: needs %zu bytes of split partials, %zu "
                      "available", who, end, bytes);
   plan->implicit = true;
+  plan->shared = false;
   plan->item_cost = decode_item_cost();
   plan->batch_size = batch_size;
   plan->hq = num_qo_heads;
@@ -999,6 +1432,50 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   }
   int cus = device_cu_count();
   if (cus <= 0) cus = 256;
+  plan->shared = false;
+
+  if (split_pages == 0 && decode_shared_mode() != 0) {
+    std::vector<SharedItem> sitems;
+    std::vector<int32_t> wg_ptr;
+    if (plan_shared(npages, hkv, head_dim, cus, decode_shared_mode() == 1, &sitems, &wg_ptr)) {
+      const int n_wg = (int)wg_ptr.size() - 1;
+      const size_t off_items = kWsHeader;
+      const size_t off_wg = ws_align(off_items + sizeof(SharedItem) * sitems.size());
+      const size_t end = ws_align(off_wg + sizeof(int32_t) * wg_ptr.size());
+      const size_t host_bytes = end - kWsHeader;
+      plan->host.assign(host_bytes / sizeof(int32_t), 0);
+      char* hb = reinterpret_cast<char*>(plan->host.data());
+      std::memcpy(hb, sitems.data(), sizeof(SharedItem) * sitems.size());
+      std::memcpy(hb + (off_wg - kWsHeader), wg_ptr.data(), sizeof(int32_t) * wg_ptr.size());
+      plan->workspace = workspace;
+      plan->workspace_bytes = workspace_bytes;
+      rc = upload_plan(plan, who, host_bytes, end, stream);
+      if (rc) return rc;
+      char* ws = static_cast<char*>(workspace);
+      plan->implicit = false;
+      plan->shared = true;
+      plan->batch_size = batch_size;
+      plan->hq = num_qo_heads;
+      plan->hkv = num_kv_heads;
+      plan->d = head_dim;
+      plan->page_size = page_size;
+      plan->n_items = n_wg;
+      plan->hg_shift = 0;
+      plan->n_merge = 0;
+      plan->n_slots = 0;
+      plan->split_pages = split_pages;
+      plan->items_dev = ws + off_items;
+      plan->wave_ptr_dev = reinterpret_cast<const int32_t*>(ws + off_wg);
+      plan->merge_dev = nullptr;
+      plan->partial_o = nullptr;
+      plan->partial_lse = nullptr;
+      plan->total_pages = total;
+      plan->max_pages = maxp;
+      plan->mode = kPlanDecode;
+      return PAGEDATTN_OK;
+    }
+  }
+
   // work is planned per head group: hg KV heads walked together by hg waves
   const int hg = decode_head_group(hkv);
   const int hg_shift = hg == 4 ? 2 : hg == 2 ? 1 : 0;
@@ -1176,6 +1653,12 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   return PAGEDATTN_OK;
 }
 
+int pagedattn_decode_plan_kind(const pagedattn_plan* plan) {
+  if (!plan || plan->mode != kPlanDecode) return 0;
+  if (plan->implicit) return PAGEDATTN_DECODE_DEVICE;
+  return plan->shared ? PAGEDATTN_DECODE_SHARED : PAGEDATTN_DECODE_SPLIT;
+}
+
 int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
                                  int32_t num_qo_heads, int32_t num_kv_heads,
                                  int32_t head_dim, int32_t page_size, void* workspace,
@@ -1295,6 +1778,14 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
 
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = q_dtype == PAGEDATTN_BF16;
+  if (plan->shared) {
+    DecodeFn fn = pick_decode_shared(plan->d, bf16, fp8, app != nullptr, app && app->rope);
+    if (!fn)
+      return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: shared-item plan for D = %d", who,
+                       plan->d);
+    hipLaunchKernelGGL(fn, dim3(plan->n_items), dim3(256), 0, s, p);
+    return check_launch(who);
+  }
   DecodeFn fn = pick_decode(plan->d, bf16, fp8, app != nullptr, app && app->rope,
                             plan->implicit);
   const int blocks = ((plan->n_items << plan->hg_shift) + 3) / 4;

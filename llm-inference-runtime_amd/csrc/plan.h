@@ -59,6 +59,9 @@ struct pagedattn_plan {
   // decode, implicit: page-equivalents charged per (sequence, head group)
   // segment by the device-side split
   int item_cost = 0;
+  // decode: whole (sequence, KV head) items shared by the waves of one
+  // workgroup per CU (n_items = workgroups; no split partials, no merge)
+  bool shared = false;
   // prefill: query tokens per tile (rows = tokens * hq/hkv)
   int q_tile = 0;
   int64_t total_qo = 0;

@@ -631,6 +631,15 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
 
     begin_forward = plan
 
+    @property
+    def plan_kind(self) -> str | None:
+        """The partition the current plan holds: "split" (head-group work
+        list, cut sequences merged by a second launch), "shared" (whole
+        (sequence, KV head) items per CU workgroup, one launch), "device"
+        (partitioned on the device at run time), or None before plan()."""
+        k = _lib.lib().pagedattn_decode_plan_kind(self._plan.handle)
+        return {1: "split", 2: "shared", 3: "device"}.get(int(k))
+
     def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, *,
             kv_scales: torch.Tensor | None = None, out: torch.Tensor | None = None,
             lse: torch.Tensor | None = None, return_lse: bool = False,
