@@ -50,6 +50,7 @@ struct DecodeParams {
   const int32_t* wave_ptr;  // [n_groups + 1]: items of head group w
   int32_t n_groups, n_merge, n_slots, batch_size;
   int32_t hg_shift;  // log2(waves per head group), 0..2
+  int32_t deterministic;  // shared plans: fixed chunk assignment
   int32_t item_cost;  // implicit partition: header units per segment
   const uint16_t* q;
   int64_t q_sn, q_sh;
@@ -768,6 +769,7 @@ struct SharedItem {
 template <int D>
 struct SharedLds {
   int total;      // chunks of the workgroup's items
+  int next;       // chunk counter (claims in arrival order)
   int tag[kSharedSlots];   // item index the slot is open for
   int cnt[kSharedSlots];   // chunks accounted for by the states left in the slot
   int mask[kSharedSlots];  // waves whose states are in the slot
@@ -839,6 +841,7 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
       L.new_pos[t] = new_pos;
       if (t == n_it - 1) L.total = it.chunk_lo + max(it.n_chunks, 0);
     }
+    if (t == 0) L.next = 0;
     if (t < kSharedSlots) {
       L.tag[t] = t;
       L.cnt[t] = 0;
@@ -875,13 +878,23 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
       qtmp[k][ks] = *reinterpret_cast<const u32x4*>(qrow + 32 * ks + 8 * G);
   }
 
-  // wave w takes chunks w, w + 4, w + 8, ... of the sequence: a fixed
-  // assignment, so the states merged per item (and the output bits) do not
-  // depend on timing
+  // chunks are claimed in arrival order through an LDS counter, so a wave
+  // that streams more slowly takes fewer (TinyLlama B=256 step 54.4-55.0 us
+  // against 56.0-56.8 us with a fixed assignment, same runs); with
+  // p.deterministic wave w takes chunks w, w + 4, w + 8, ..., so the states
+  // merged per item (and the output bits) do not depend on timing
   int next_chunk = wave;
   auto claim = [&]() -> ChunkRef {
-    const int c = next_chunk;
-    next_chunk += 4;
+    int c;
+    if (p.deterministic) {
+      c = next_chunk;
+      next_chunk += 4;
+    } else {
+      c = 0;
+      if (lane == 0)
+        c = __hip_atomic_fetch_add(&L.next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      c = uniform(c);
+    }
     if (c >= total) return ChunkRef{-1, 0};
     const int cnt = (int)__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < n_it && t_lo <= c));
     const int it = uniform(cnt > 0 ? cnt - 1 : 0);
@@ -1045,14 +1058,14 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
   // ---- chunks: two register stages, the next chunk's loads in flight while
   // the current one is computed, page ids one chunk further ahead
   while (ra.item >= 0) {
+    load(sb, idb, rb);
     ChunkRef rc = claim();
     fetch(ida, rc);
-    load(sb, idb, rb);
     compute(sa, ra);
     if (rb.item < 0) break;
+    load(sa, ida, rc);
     ChunkRef rd = claim();
     fetch(idb, rd);
-    load(sa, ida, rc);
     compute(sb, rb);
     ra = rc;
     rb = rd;
@@ -1277,6 +1290,14 @@ static int decode_shared_mode() {
   }
   return -1;
 }
+// Shared plans claim chunks in arrival order (fastest);
+// PAGEDATTN_DECODE_DETERMINISTIC=1 gives them a fixed chunk assignment,
+// whose output bits do not depend on timing.
+static bool decode_deterministic() {
+  const char* env = std::getenv("PAGEDATTN_DECODE_DETERMINISTIC");
+  return env && std::atoi(env) == 1;
+}
+
 static int64_t decode_shared_slack_bytes() {
   if (const char* env = std::getenv("PAGEDATTN_DECODE_SHARED_SLACK_KB")) {
     const int v = std::atoi(env);
@@ -1450,6 +1471,7 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
       char* ws = static_cast<char*>(workspace);
       plan->implicit = false;
       plan->shared = true;
+      plan->deterministic = decode_deterministic();
       plan->batch_size = batch_size;
       plan->hq = num_qo_heads;
       plan->hkv = num_kv_heads;
@@ -1739,6 +1761,7 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   p.wave_ptr = plan->wave_ptr_dev;
   p.n_groups = plan->n_items;
   p.hg_shift = plan->hg_shift;
+  p.deterministic = plan->deterministic ? 1 : 0;
   p.item_cost = plan->item_cost;
   p.n_merge = plan->n_merge;
   p.n_slots = plan->n_slots;

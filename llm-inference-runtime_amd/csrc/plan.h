@@ -62,6 +62,8 @@ struct pagedattn_plan {
   // decode: whole (sequence, KV head) items shared by the waves of one
   // workgroup per CU (n_items = workgroups; no split partials, no merge)
   bool shared = false;
+  // decode, shared: fixed chunk assignment (output bits independent of timing)
+  bool deterministic = false;
   // prefill: query tokens per tile (rows = tokens * hq/hkv)
   int q_tile = 0;
   int64_t total_qo = 0;
