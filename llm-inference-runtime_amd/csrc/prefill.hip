@@ -376,6 +376,11 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       ksc_l = kr.sc;
       vsc_l = vr.sc;
     }
+    // Every wave's direct-to-LDS loads of tile t are complete before any wave
+    // passes the barrier and reads them.  The barrier itself waits only for
+    // LDS operations (workgroup-scope release), so this wait is explicit
+    // rather than left to the compiler's alias tracking of the loads.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
     const bool more = t + 1 < n_tiles;
     pid = pid_next;
