@@ -97,8 +97,10 @@ def _device_plan_run(gpu, meta, pool, q, hq, hkv, d, kv_scales=None):
 ])
 def test_device_plan_equals_host_plan(gpu, name, lens, hq, hkv, d, monkeypatch):
     # the device partition cuts equal page shares; the host planner's
-    # balanced split does the same with no per-item charge
+    # balanced split does the same with no per-item charge (a split plan:
+    # shared-item plans are another partition)
     monkeypatch.setenv("PAGEDATTN_DECODE_ITEM_COST", "0")
+    monkeypatch.setenv("PAGEDATTN_DECODE_SHARED", "0")
     lens = [int(x) for x in lens]
     meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=len(lens))
     got, got_lse = _device_plan_run(gpu, meta, pool, q, hq, hkv, d)
@@ -122,6 +124,7 @@ def test_device_plan_item_cost(gpu, monkeypatch, cost, name, lens, hq, hkv, d):
     # (sequence, head group) segment) is still a partition: oracle answer,
     # and the host plan's answer to the rounding of the merges
     monkeypatch.setenv("PAGEDATTN_DECODE_ITEM_COST", cost)
+    monkeypatch.setenv("PAGEDATTN_DECODE_SHARED", "0")
     lens = [int(x) for x in lens]
     meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=len(lens) + 1)
     got, got_lse = _device_plan_run(gpu, meta, pool, q, hq, hkv, d)
@@ -135,6 +138,7 @@ def test_device_plan_item_cost(gpu, monkeypatch, cost, name, lens, hq, hkv, d):
 
 def test_device_plan_e4m3(gpu, monkeypatch):
     monkeypatch.setenv("PAGEDATTN_DECODE_ITEM_COST", "0")
+    monkeypatch.setenv("PAGEDATTN_DECODE_SHARED", "0")
     lens = [int(x) for x in np.random.default_rng(7).integers(1, 8192, 32)]
     meta, pool, q = decode_case(gpu, lens, 64, 8, 128, seed=7)
     q8, scales = pagedattn.quantize_pages_e4m3(pool)
