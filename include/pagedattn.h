@@ -277,7 +277,9 @@ int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
  * split_pages = 0 takes a shared plan at head_dim 64 when its busiest CU
  * carries at most PAGEDATTN_DECODE_SHARED_SLACK_KB (environment, default 96)
  * KiB more K/V than the mean; PAGEDATTN_DECODE_SHARED=0 / =1 turns that off
- * / takes one whenever it fits. */
+ * / takes one whenever it fits.  A shared plan's waves take page pairs in
+ * arrival order, so repeated runs can differ in the last bits of the output;
+ * PAGEDATTN_DECODE_DETERMINISTIC=1 (read at plan time) fixes the order. */
 #define PAGEDATTN_DECODE_SPLIT 1
 #define PAGEDATTN_DECODE_SHARED 2
 #define PAGEDATTN_DECODE_DEVICE 3
