@@ -214,9 +214,10 @@ int pagedattn_fork_pages(void* kv_pool, int32_t pool_dtype, int32_t num_layers,
  *     new token counts,
  *   batch_indices / positions [tokens_capacity]: sequence and position of
  *     every new token (kv_lens[b] - n .. kv_lens[b] - 1).
- * Two launches with fixed shapes (graph-capturable).  A row needing more
- * than max_pages pages, or outputs beyond a capacity, are dropped and
- * counted in *error_flag. */
+ * One launch for batches up to 1024 sequences, two above, all with fixed
+ * shapes (graph-capturable).  A row needing more than max_pages pages is
+ * cut to them and outputs beyond a capacity are dropped; both are counted in
+ * *error_flag. */
 int pagedattn_build_paged_metadata(const int32_t* block_tables, int64_t table_stride,
                                    int32_t max_pages, const int32_t* kv_lens,
                                    const int32_t* new_lens, int32_t batch_size,

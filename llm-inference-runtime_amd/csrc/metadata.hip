@@ -142,6 +142,81 @@ __global__ void __launch_bounds__(256) meta_fill_kernel(MetaArgs a) {
   if (__syncthreads_or(over) && threadIdx.x == 0 && a.err) atomicAdd(a.err, 1);
 }
 
+// Batches up to kMetaFuseMax sequences: one launch, grid (x, b).  Every
+// workgroup of sequence b sums the page and token counts of the sequences
+// before it itself (at most kMetaFuseMax loads per workgroup), so no
+// workgroup waits for another; then it writes what the scan and the fill
+// kernels write for b.  A clipped row is counted once per sequence.
+constexpr int kMetaFuseMax = 1024;
+constexpr int kMetaFuseThreads = 256;
+
+__global__ void __launch_bounds__(kMetaFuseThreads) meta_fused_kernel(MetaArgs a) {
+  __shared__ int red[2][kMetaFuseThreads / kWave];
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  int sp = 0, st = 0;
+  for (int i = (int)threadIdx.x; i < b; i += kMetaFuseThreads) {
+    const int Li = a.kv_lens[i];
+    sp += seq_pages(a, Li);
+    st += seq_new_tokens(a, i, Li);
+  }
+#pragma unroll
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    sp += __shfl_xor(sp, o);
+    st += __shfl_xor(st, o);
+  }
+  if (lane == 0) {
+    red[0][wave] = sp;
+    red[1][wave] = st;
+  }
+  __syncthreads();
+  int off = 0, qo = 0;
+#pragma unroll
+  for (int w = 0; w < kMetaFuseThreads / kWave; ++w) {
+    off += red[0][w];
+    qo += red[1][w];
+  }
+  const int L = a.kv_lens[b];
+  const int np = seq_pages(a, L);
+  const int nt = seq_new_tokens(a, b, L);
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    a.kv_indptr[b] = off;
+    if (a.qo_indptr) a.qo_indptr[b] = qo;
+    a.last[b] = L > 0 ? (L - 1) % kPage + 1 : kPage;
+    if (!a.new_lens) {
+      a.bi[b] = b;
+      a.pos[b] = L - 1;
+    }
+    if (b == a.batch - 1) {
+      a.kv_indptr[a.batch] = off + np;
+      if (a.qo_indptr) a.qo_indptr[a.batch] = qo + nt;
+    }
+    const int full = L > 0 ? (L + kPage - 1) / kPage : 0;
+    if (full > np && a.err) atomicAdd(a.err, 1);
+  }
+  const int step = gridDim.x * blockDim.x;
+  const int first = blockIdx.x * blockDim.x + threadIdx.x;
+  const int32_t* row = a.tables + (int64_t)b * a.stride;
+  bool over = false;
+  for (int i = first; i < np; i += step) {
+    if (off >= 0 && (int64_t)off + i < a.indices_cap) a.kv_indices[off + i] = row[i];
+    else over = true;
+  }
+  if (a.new_lens) {
+    for (int j = first; j < nt; j += step) {
+      const int64_t t = (int64_t)qo + j;
+      if (qo >= 0 && t < a.tokens_cap) {
+        a.bi[t] = b;
+        a.pos[t] = L - nt + j;
+      } else {
+        over = true;
+      }
+    }
+  }
+  if (__syncthreads_or(over) && threadIdx.x == 0 && a.err) atomicAdd(a.err, 1);
+}
+
 }  // namespace pa
 
 using namespace pa;
@@ -180,10 +255,15 @@ int pagedattn_build_paged_metadata(const int32_t* block_tables, int64_t table_st
              qo_indptr, kv_indptr, kv_indices, indices_capacity, kv_last_page_len,
              batch_indices, positions, tokens_capacity, error_flag};
   hipStream_t s = (hipStream_t)stream;
+  const unsigned gx = (unsigned)std::max(1, std::min(64, (max_pages + 255) / 256));
+  if (batch_size > 0 && batch_size <= kMetaFuseMax) {
+    hipLaunchKernelGGL(meta_fused_kernel, dim3(gx, batch_size), dim3(kMetaFuseThreads), 0, s,
+                       a);
+    return check_launch(who);
+  }
   hipLaunchKernelGGL(meta_scan_kernel, dim3(1), dim3(kMetaThreads), 0, s, a);
   int rc = check_launch(who);
   if (rc || batch_size == 0) return rc;
-  const unsigned gx = (unsigned)std::max(1, std::min(64, (max_pages + 255) / 256));
   hipLaunchKernelGGL(meta_fill_kernel, dim3(gx, batch_size), dim3(256), 0, s, a);
   return check_launch(who);
 }
