@@ -140,7 +140,10 @@ __device__ __forceinline__ int lds_off(int r, int c) {
 template <int D, bool BF16, bool FP8, int RB>
 struct HalfRegs {
   using C = PrefillCfg<D, BF16, FP8, RB>;
-  u32x2 x[C::CPT];
+  // 16 e4m3 elements per lane and load where the tile divides evenly
+  static constexpr bool WIDE = (C::CHUNKS / 2) % C::THREADS == 0;
+  static constexpr int NL = WIDE ? C::CHUNKS / 2 / C::THREADS : C::CPT;
+  typename std::conditional<WIDE, u32x4, u32x2>::type x[NL];
   float sc;  // lane j < 4 holds the scale of the tile's page j
 };
 
@@ -204,24 +207,30 @@ __device__ __forceinline__ void dma_half(const PrefillParams& p, int h,
   }
 }
 
-// e4m3 pools: register loads of one half of a K/V tile (8 elements per
-// lane and load) plus the four page scales.
+// e4m3 pools: register loads of one half of a K/V tile (16 elements per
+// lane and load at D = 128, 8 at D = 64) plus the four page scales.
 template <int D, bool BF16, bool FP8, int RB, bool V>
 __device__ __forceinline__ void load_half(HalfRegs<D, BF16, FP8, RB>& hr,
                                           const PrefillParams& p, int h,
                                           int pid, int npages, int last,
                                           int tile, int wave, int lane) {
   using C = PrefillCfg<D, BF16, FP8, RB>;
+  using H = HalfRegs<D, BF16, FP8, RB>;
+  constexpr int E = H::WIDE ? 16 : 8;  // elements per lane and load
 #pragma unroll
-  for (int k = 0; k < C::CPT; ++k) {
+  for (int k = 0; k < H::NL; ++k) {
     const int c = lane + 64 * wave + C::THREADS * k;
-    const int tok = c / (D / 8);
-    const int d0 = (c % (D / 8)) * 8;
-    // the 64 chunks of a wave lie in one page of the tile
-    const int j = uniform((64 * wave + C::THREADS * k) / (D / 8) / kPage);
+    const int tok = c / (D / E);
+    const int d0 = (c % (D / E)) * E;
+    // the 64 pieces of a wave lie in one page of the tile
+    const int j = uniform((64 * wave + C::THREADS * k) / (D / E) / kPage);
     const __amdgpu_buffer_rsrc_t r =
         page_rsrc<D, BF16, FP8, RB, V>(p, h, pid, npages, last, tile, j);
-    hr.x[k] = buf_load8(r, (uint32_t)((tok % kPage) * D + d0));
+    if constexpr (H::WIDE) {
+      hr.x[k] = buf_load16(r, (uint32_t)((tok % kPage) * D + d0));
+    } else {
+      hr.x[k] = buf_load8(r, (uint32_t)((tok % kPage) * D + d0));
+    }
   }
   hr.sc = 0.f;
   if (lane < 4 && pid >= 0 && pid < p.num_pages)
@@ -233,17 +242,22 @@ template <int D, bool BF16, bool FP8, int RB>
 __device__ __forceinline__ void store_half(const HalfRegs<D, BF16, FP8, RB>& hr,
                                            uint8_t* lds, int wave, int lane) {
   using C = PrefillCfg<D, BF16, FP8, RB>;
+  using H = HalfRegs<D, BF16, FP8, RB>;
+  constexpr int E = H::WIDE ? 16 : 8;
 #pragma unroll
-  for (int k = 0; k < C::CPT; ++k) {
+  for (int k = 0; k < H::NL; ++k) {
     const int c = lane + 64 * wave + C::THREADS * k;
-    const int tok = c / (D / 8);
-    const int chunk = c % (D / 8);
-    u32x4 x;
-    x[0] = e4m3x2_to16<BF16, false>(hr.x[k][0]);
-    x[1] = e4m3x2_to16<BF16, true>(hr.x[k][0]);
-    x[2] = e4m3x2_to16<BF16, false>(hr.x[k][1]);
-    x[3] = e4m3x2_to16<BF16, true>(hr.x[k][1]);
-    *reinterpret_cast<u32x4*>(lds + lds_off<D>(tok, chunk)) = x;
+    const int tok = c / (D / E);
+    const int chunk = (c % (D / E)) * (E / 8);
+#pragma unroll
+    for (int q = 0; q < E / 8; ++q) {
+      u32x4 x;
+      x[0] = e4m3x2_to16<BF16, false>(hr.x[k][2 * q]);
+      x[1] = e4m3x2_to16<BF16, true>(hr.x[k][2 * q]);
+      x[2] = e4m3x2_to16<BF16, false>(hr.x[k][2 * q + 1]);
+      x[3] = e4m3x2_to16<BF16, true>(hr.x[k][2 * q + 1]);
+      *reinterpret_cast<u32x4*>(lds + lds_off<D>(tok, chunk + q)) = x;
+    }
   }
 }
 
