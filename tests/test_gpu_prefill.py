@@ -80,6 +80,20 @@ def test_prefill_llama3_8b_chunked(gpu):
     assert lse_err(lse, ref_l) <= TOL_LSE
 
 
+def test_prefill_tinyllama_shape(gpu):
+    # the reference engine's default model (TinyLlama: 32 query heads, 4 KV
+    # heads, head_dim 64) on chunked prefills over long and short prefixes,
+    # partial pages included; oracle on every row
+    computed = [0, 16, 256, 1000, 2048, 37, 512, 3000]
+    chunks = [512, 300, 129, 64, 256, 400, 33, 128]
+    meta, pool, q = prefill_case(gpu, computed, chunks, 32, 4, 64, seed=64)
+    out, lse = run_prefill(gpu, meta, pool, q, 32, 4, 64)
+    ref_o, ref_l = oracle_prefill(meta, pool, q)
+    assert max_err(out, ref_o) <= TOL_BF16
+    assert rel_err(out, ref_o) <= TOL_REL_BF16
+    assert lse_err(lse, ref_l) <= TOL_LSE
+
+
 def test_prefill_split_chunk_equivalence(gpu):
     # size-independent: prefilling a chunk at once equals prefilling its two
     # halves one after the other (the second half attends to the first)
