@@ -271,3 +271,29 @@ def test_prefill_zero_q_is_causal_mean_of_v(gpu):
         seen = torch.arange(n - qo + 1, n + 1, device=gpu, dtype=torch.float64)
         want = (csum[n - qo:] / seen[:, None, None]).float().repeat_interleave(gq, dim=1)
         _check_close(out[m.qo_indptr[b]:m.qo_indptr[b + 1]], want)
+
+
+@pytest.mark.parametrize("kind", ["decode", "prefill"])
+def test_fp16_pools_zero_q_is_mean_of_v(gpu, kind):
+    # the fp16 kernels at full size: TinyLlama decode and the Llama-3-8B
+    # prefill with fp16 pool and q
+    w = W.tinyllama_decode(seed=13) if kind == "decode" else W.llama3_8b_prefill(seed=13)
+    t = W.materialize(w, gpu, dtype=torch.float16)
+    m = w.meta
+    q = torch.zeros_like(t.q)
+    gq = w.hq // w.hkv
+    if kind == "decode":
+        out, _, _ = _decode(gpu, w, t.pool, t, t.kv_indices, q)
+        for b in range(m.batch_size):
+            want = _v_rows(t.pool, m, b).mean(dim=0).repeat_interleave(gq, dim=0)
+            _check_close(out[b], want)
+    else:
+        out, _ = _prefill(gpu, w, t.pool, t, t.kv_indices, q)
+        for b in range(m.batch_size):
+            v = _v_rows(t.pool, m, b).double()
+            n = v.shape[0]
+            qo = int(m.qo_indptr[b + 1] - m.qo_indptr[b])
+            csum = torch.cumsum(v, dim=0)
+            seen = torch.arange(n - qo + 1, n + 1, device=gpu, dtype=torch.float64)
+            want = (csum[n - qo:] / seen[:, None, None]).float().repeat_interleave(gq, dim=1)
+            _check_close(out[m.qo_indptr[b]:m.qo_indptr[b + 1]], want)
