@@ -1,7 +1,8 @@
 """CPU oracle of the paged-attention path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this package, and only as the checker (or the timed CPU baseline):
+import this package, and only as the reference that GPU results are compared with (or the timed
+CPU baseline):
 the product path (llm-inference-runtime_amd/pagedattn) never imports it and
 fails loudly when libpagedattn.so is missing.
 

@@ -1,5 +1,5 @@
-"""Pins the CPU oracle (oracle/paged_ref.py) before it is trusted as the
-checker: closed forms, pure-Python loops, fp64 brute-force golden vectors
+"""Pins the CPU oracle (oracle/paged_ref.py) before GPU results are compared
+with it: closed forms, pure-Python loops, fp64 brute-force golden vectors
 (tests/golden/), invariants, transformers' RoPE, and planted mistakes that
 these pins must catch."""
 
