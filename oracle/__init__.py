@@ -1,10 +1,10 @@
 """CPU oracle of the paged-attention path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
-import this package, and only as the reference that GPU results are compared with (or the timed
-CPU baseline):
-the product path (llm-inference-runtime_amd/pagedattn) never imports it and
-fails loudly when libpagedattn.so is missing.
+import this package, and only as the reference that GPU results are
+compared with (or the timed CPU baseline): the product path
+(llm-inference-runtime_amd/pagedattn) never imports it and fails loudly
+when libpagedattn.so is missing.
 
 The reference's arithmetic lives in flashinfer-python 0.6.11.post3
 (pyproject.toml:13, uv.lock:526-547), which is not vendored and is CUDA-only,
