@@ -27,6 +27,7 @@
 #include <algorithm>
 #include <climits>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <type_traits>
 #include <vector>
@@ -178,11 +179,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(
   return make_rsrc(base, (uint32_t)(ntok * D * C::ESZ));
 }
 
-// bf16/fp16 pools: direct-to-LDS loads of one half of a K/V tile.  Wave w's
-// k-th load fills the 1 KiB block 8 k + w of the tile (lane i -> bytes
-// [16 i, 16 i + 16) of the block), so each lane fetches the global chunk
-// that the swizzle puts at its position.
-template <int D, bool BF16, bool FP8, int RB, bool V>
+// bf16/fp16 pools: direct-to-LDS loads of one half of a K/V tile by a group
+// of NW waves.  Wave w's k-th load fills the 1 KiB block NW k + w of the tile
+// (lane i -> bytes [16 i, 16 i + 16) of the block), so each lane fetches the
+// global chunk that the swizzle puts at its position.
+template <int D, bool BF16, bool FP8, int RB, bool V, int NW>
 __device__ __forceinline__ void dma_half(const PrefillParams& p, int h,
                                          int pid, int npages, int last,
                                          int tile, uint8_t* lds, int wave,
@@ -190,10 +191,10 @@ __device__ __forceinline__ void dma_half(const PrefillParams& p, int h,
   using C = PrefillCfg<D, BF16, FP8, RB>;
   constexpr int RPB = 1024 / C::ROWB;   // rows per 1 KiB block
   constexpr int CPR = C::ROWB / 16;     // chunks per row
-  constexpr int NK = C::TILEB / 1024 / C::WAVES;
+  constexpr int NK = C::TILEB / 1024 / NW;
 #pragma unroll
   for (int k = 0; k < NK; ++k) {
-    const int blk = C::WAVES * k + wave;
+    const int blk = NW * k + wave;
     const int row0 = blk * RPB;
     const int j = uniform(row0 / kPage);  // page of the block within the tile
     const __amdgpu_buffer_rsrc_t r =
@@ -282,6 +283,12 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
   // does not wait for them before those reads.
   __shared__ __attribute__((aligned(1024))) uint8_t stage0[2 * C::TILEB];
   __shared__ __attribute__((aligned(1024))) uint8_t stage1[2 * C::TILEB];
+  // The second head's stages of a paired tile.  Pairing is built for
+  // 16-bit pools at D = 128 only: at D = 64 its registers would cost the
+  // second workgroup per CU.
+  constexpr bool PAIRS = !FP8 && D == 128;
+  __shared__ __attribute__((aligned(1024))) uint8_t stage2[PAIRS ? 2 * C::TILEB : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t stage3[PAIRS ? 2 * C::TILEB : 16];
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -315,6 +322,21 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
   const int clean_end =
       p.causal ? min(kv_len, max(0, diag + q_lo + 1)) : kv_len;
   const int n_tiles = (kv_end + BN - 1) / BN;
+  // A paired tile (flagged by the planner; at most half the workgroup's rows)
+  // is run for KV heads h and h + 1 by the even-head workgroup: waves
+  // 0 .. WAVES/2 - 1 take head h, the others head h + 1, each group with its
+  // own K/V stages.  Both groups walk the same tiles, so they meet at every
+  // barrier.  The odd-head workgroup has nothing left to do.
+  const bool paired = PAIRS && (p.hkv & 1) == 0 &&
+                      uniform(load_invariant(itp + 3)) == 1 &&
+                      (q_hi - q_lo) * g <= C::ROWS / 2;
+  if (paired && (h & 1)) return;
+
+  // The tile loop of one head group: NW waves, wave index `wave` within the
+  // group, KV head `h`, LDS stages st0 / st1.
+  auto body = [&](auto pair_tag, uint8_t* st0, uint8_t* st1, const int wave,
+                  const int h) __attribute__((always_inline)) {
+  constexpr int NW = decltype(pair_tag)::value ? C::WAVES / 2 : C::WAVES;
 
   // ---- Q^T fragments (B operand): lane -> row, 8 consecutive d per k-step
   u32x4 qf[RB][C::KS];
@@ -374,9 +396,9 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       load_half<D, BF16, FP8, RB, false>(kr, p, h, pid, npages, last, 0, wave, lane);
       load_half<D, BF16, FP8, RB, true>(vr, p, h, pid, npages, last, 0, wave, lane);
     } else {
-      dma_half<D, BF16, FP8, RB, false>(p, h, pid, npages, last, 0, stage0, wave, lane);
-      dma_half<D, BF16, FP8, RB, true>(p, h, pid, npages, last, 0, stage0 + C::TILEB,
-                                       wave, lane);
+      dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid, npages, last, 0, st0, wave, lane);
+      dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid, npages, last, 0, st0 + C::TILEB,
+                                           wave, lane);
     }
   }
   int pid_next = fetch_page_ids(p, ind_lo, npages, 1, lane);
@@ -417,7 +439,8 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
         if constexpr (FP8) {
           load_half<D, BF16, FP8, RB, false>(kr, p, h, pid, npages, last, t + 1, wave, lane);
         } else {
-          dma_half<D, BF16, FP8, RB, false>(p, h, pid, npages, last, t + 1, nxt, wave, lane);
+          dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid, npages, last, t + 1, nxt, wave,
+                                                lane);
         }
       }
     }
@@ -487,8 +510,8 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
         if constexpr (FP8) {
           load_half<D, BF16, FP8, RB, true>(vr, p, h, pid, npages, last, t + 1, wave, lane);
         } else {
-          dma_half<D, BF16, FP8, RB, true>(p, h, pid, npages, last, t + 1, nxt + C::TILEB,
-                                           wave, lane);
+          dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid, npages, last, t + 1,
+                                               nxt + C::TILEB, wave, lane);
         }
       }
       u32x4 pb[RB];
@@ -516,9 +539,9 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
     }
   };
   for (int t = 0; t < n_tiles; t += 2) {
-    step(t, stage0, stage1);
+    step(t, st0, st1);
     if (t + 1 >= n_tiles) break;
-    step(t + 1, stage1, stage0);
+    step(t + 1, st1, st0);
   }
 
   // ---- epilogue: O^T / l, lane's row, 4 consecutive d per register quad
@@ -545,6 +568,18 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       p.lse[(int64_t)(qo_start + qi) * p.hq + head] =
           l_tot > 0.f ? (m[rb] + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
   }
+  };
+
+  if constexpr (PAIRS) {
+    if (paired) {
+      if (wave < C::WAVES / 2)
+        body(std::true_type{}, stage0, stage1, wave, h);
+      else
+        body(std::true_type{}, stage2, stage3, wave - C::WAVES / 2, h + 1);
+      return;
+    }
+  }
+  body(std::false_type{}, stage0, stage1, wave, h);
 }
 
 using PrefillFn = void (*)(PrefillParams);
@@ -566,6 +601,14 @@ static PrefillFn pick_prefill(int d, bool bf16, bool fp8) {
 }
 
 constexpr int kPrefillRows = kPrefillWaves * 32 * kPrefillRB;
+
+// Paired tiles (a q-tile of at most half a workgroup's rows, run for two KV
+// heads by one workgroup) are planned by default; PAGEDATTN_PREFILL_PAIR=0
+// plans every tile on its own.
+static bool prefill_pairing() {
+  const char* env = std::getenv("PAGEDATTN_PREFILL_PAIR");
+  return !(env && std::atoi(env) == 0);
+}
 
 }  // namespace pa
 
@@ -602,6 +645,7 @@ int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
     return set_error(PAGEDATTN_ERR_INVALID, "%s: qo_indptr[0] < 0", who);
   const int g = num_qo_heads / num_kv_heads;
   const int q_tile = kPrefillRows / g;
+  const bool pair = prefill_pairing() && num_kv_heads % 2 == 0;
   std::vector<PrefillItem> items;
   std::vector<int64_t> cost;
   for (int b = 0; b < batch_size; ++b) {
@@ -611,7 +655,10 @@ int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
                        "%s: qo_indptr is not monotone at %d", who, b);
     for (int lo = 0; lo < qo; lo += q_tile) {
       const int hi = std::min(qo, lo + q_tile);
-      items.push_back(PrefillItem{b, lo, hi, -1});
+      // slot 1: a paired tile (kernels built without pairing -- e4m3 pools,
+      // D = 64 -- run it like any other)
+      const int flag = pair && (int64_t)(hi - lo) * g <= kPrefillRows / 2 ? 1 : -1;
+      items.push_back(PrefillItem{b, lo, hi, flag});
       // kv tokens the tile's last row can see (causal)
       cost.push_back(std::max<int64_t>(
           0, std::min<int64_t>(kv_len[b], (int64_t)kv_len[b] - qo + hi)));

@@ -156,3 +156,25 @@ def test_prefill_rescale_branch(gpu, fp8, d, hq, hkv):
     assert max_err(out, ref_o) <= tol
     assert rel_err(out, ref_o) <= tol_rel
     assert lse_err(lse, ref_l) <= lse_tol
+
+
+@pytest.mark.parametrize("case", ["edges", "llama3_8b"])
+@pytest.mark.parametrize("causal", [True, False])
+def test_prefill_paired_tiles_bit_identical(gpu, monkeypatch, case, causal):
+    # q-tiles with at most half a workgroup's rows run two KV heads in one
+    # workgroup (D = 128, 16-bit pools); each row's arithmetic is unchanged,
+    # so output and LSE bits equal the unpaired plan's
+    if case == "edges":
+        computed = [c for c, _ in EDGE] + [2000, 37]
+        chunks = [n for _, n in EDGE] + [20, 45]
+        hq, hkv, d = 32, 8, 128
+        meta, pool, q = prefill_case(gpu, computed, chunks, hq, hkv, d, seed=77)
+    else:
+        w = W.llama3_8b_prefill(seed=5)
+        t = W.materialize(w, gpu)
+        meta, pool, q, hq, hkv, d = w.meta, t.pool, t.q, w.hq, w.hkv, w.d
+    out1, lse1 = run_prefill(gpu, meta, pool, q, hq, hkv, d, causal=causal)
+    monkeypatch.setenv("PAGEDATTN_PREFILL_PAIR", "0")
+    out0, lse0 = run_prefill(gpu, meta, pool, q, hq, hkv, d, causal=causal)
+    assert torch.equal(out0, out1)
+    assert torch.equal(lse0, lse1)
