@@ -351,7 +351,10 @@ int pagedattn_decode_run_rope_append(
 
 /* BatchPrefillWithPagedKVCacheWrapper.begin_forward(qo_indptr, kv_indptr,
  *     kv_indices, kv_last_page_len, Hq, Hkv, D, page_size, q_data_type)
- *     (src/models/llama.py:86-116).  Host copies of the indptr arrays. */
+ *     (src/models/llama.py:86-116).  Host copies of the indptr arrays.
+ * q-tiles of at most half a workgroup's rows are planned as pairs of KV
+ * heads sharing one workgroup when num_kv_heads is even (same output bits);
+ * PAGEDATTN_PREFILL_PAIR=0, read at plan time, plans every tile alone. */
 int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
                            const int32_t* kv_indptr_host,
                            const int32_t* kv_last_page_len_host,
