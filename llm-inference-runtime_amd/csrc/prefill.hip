@@ -336,238 +336,238 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
   // group, KV head `h`, LDS stages st0 / st1.
   auto body = [&](auto pair_tag, uint8_t* st0, uint8_t* st1, const int wave,
                   const int h) __attribute__((always_inline)) {
-  constexpr int NW = decltype(pair_tag)::value ? C::WAVES / 2 : C::WAVES;
+    constexpr int NW = decltype(pair_tag)::value ? C::WAVES / 2 : C::WAVES;
 
-  // ---- Q^T fragments (B operand): lane -> row, 8 consecutive d per k-step
-  u32x4 qf[RB][C::KS];
-  int lim[RB];       // last visible kv index of the lane's row
-  bool rvalid[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const int row = 32 * (RB * wave + rb) + col;
-    const int qi = q_lo + row / g;
-    rvalid[rb] = qi < q_hi;
-    lim[rb] = p.causal ? min(diag + qi, kv_len - 1) : kv_len - 1;
-    const uint16_t* qp =
-        p.q + (int64_t)(qo_start + (rvalid[rb] ? qi : q_lo)) * p.q_sn +
-        (int64_t)(h * g + row % g) * p.q_sh + 8 * half;
-#pragma unroll
-    for (int ks_ = 0; ks_ < C::KS; ++ks_) {
-      u32x4 z = {0u, 0u, 0u, 0u};
-      if (rvalid[rb]) z = *reinterpret_cast<const u32x4*>(qp + 16 * ks_);
-      qf[rb][ks_] = z;
-    }
-  }
-
-  f32x16 o[RB][C::DT];
-  float m[RB], l[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt) o[rb][dt] = f32x16{};
-    m[rb] = -INFINITY;
-    l[rb] = 0.f;
-  }
-
-  // Per-lane LDS byte offsets (swizzled) of the MFMA operand reads, fixed
-  // for the whole loop: K rows 32 mt + col, chunk 2 ks + half (mt adds
-  // 32 rows, which keeps the swizzle); V transpose reads at rows
-  // 16 st + 4 half + L/4 (+8), chunk 4 dt + 2 (qg & 1) + (L & 3) / 2.
-  int koff[C::KS];
-#pragma unroll
-  for (int ks_ = 0; ks_ < C::KS; ++ks_) koff[ks_] = lds_off<D>(col, 2 * ks_ + half);
-  const int L = lane & 15;
-  const int qg = lane >> 4;
-  int voff[C::DT][2];
-#pragma unroll
-  for (int dt = 0; dt < C::DT; ++dt)
-#pragma unroll
-    for (int hi = 0; hi < 2; ++hi)
-      voff[dt][hi] = C::TILEB +
-                     lds_off<D>(4 * half + (L >> 2) + 8 * hi,
-                                4 * dt + 2 * (qg & 1) + ((L & 3) >> 1)) +
-                     8 * (L & 1);
-
-  HalfRegs<D, BF16, FP8, RB> kr, vr;  // e4m3 staging only
-  float ksc_l = 0.f, vsc_l = 0.f;     // e4m3 scales of the computed tile
-  int pid = fetch_page_ids(p, ind_lo, npages, 0, lane);
-  if (n_tiles > 0) {
-    if constexpr (FP8) {
-      load_half<D, BF16, FP8, RB, false>(kr, p, h, pid, npages, last, 0, wave, lane);
-      load_half<D, BF16, FP8, RB, true>(vr, p, h, pid, npages, last, 0, wave, lane);
-    } else {
-      dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid, npages, last, 0, st0, wave, lane);
-      dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid, npages, last, 0, st0 + C::TILEB,
-                                           wave, lane);
-    }
-  }
-  int pid_next = fetch_page_ids(p, ind_lo, npages, 1, lane);
-
-  // Iteration t: (e4m3: convert and store tile t) -- barrier -- issue tile
-  // t + 1's loads into the other stage, interleaved with tile t's MFMAs.
-  auto step = [&](int t, uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
-    if constexpr (FP8) {
-      store_half<D, BF16, FP8, RB>(kr, cur, wave, lane);
-      store_half<D, BF16, FP8, RB>(vr, cur + C::TILEB, wave, lane);
-      ksc_l = kr.sc;
-      vsc_l = vr.sc;
-    }
-    // Every wave's direct-to-LDS loads of tile t are complete before any wave
-    // passes the barrier and reads them.  The barrier itself waits only for
-    // LDS operations (workgroup-scope release), so this wait is explicit
-    // rather than left to the compiler's alias tracking of the loads.
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    const bool more = t + 1 < n_tiles;
-    pid = pid_next;
-    pid_next = fetch_page_ids(p, ind_lo, npages, t + 2, lane);
-
-    // ---- S^T = K . Q^T
-    f32x16 s[RB][2];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) s[rb][0] = s[rb][1] = f32x16{};
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-      for (int ks_ = 0; ks_ < C::KS; ++ks_) {
-        const u32x4 a =
-            *reinterpret_cast<const u32x4*>(cur + 32 * mt * C::ROWB + koff[ks_]);
-#pragma unroll
-        for (int rb = 0; rb < RB; ++rb) s[rb][mt] = mfma32<BF16>(a, qf[rb][ks_], s[rb][mt]);
-      }
-      if (mt == 0 && more) {
-        if constexpr (FP8) {
-          load_half<D, BF16, FP8, RB, false>(kr, p, h, pid, npages, last, t + 1, wave, lane);
-        } else {
-          dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid, npages, last, t + 1, nxt, wave,
-                                                lane);
-        }
-      }
-    }
-
-    // ---- online softmax in log2 units; lane holds 32 of the tile's 64
-    // tokens of its row (token 32 mt + 8 (i/4) + 4 half + i%4 in register i)
-    const int tok0 = t * BN;
-    const bool need_mask = tok0 + BN > clean_end;
-    float ksc[4], vsc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      ksc[i] = FP8 ? lane_value(ksc_l, i) * p.scale_log2 : p.scale_log2;
-      vsc[i] = FP8 ? lane_value(vsc_l, i) : 1.f;
-    }
+    // ---- Q^T fragments (B operand): lane -> row, 8 consecutive d per k-step
+    u32x4 qf[RB][C::KS];
+    int lim[RB];       // last visible kv index of the lane's row
+    bool rvalid[RB];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
+      const int row = 32 * (RB * wave + rb) + col;
+      const int qi = q_lo + row / g;
+      rvalid[rb] = qi < q_hi;
+      lim[rb] = p.causal ? min(diag + qi, kv_len - 1) : kv_len - 1;
+      const uint16_t* qp =
+          p.q + (int64_t)(qo_start + (rvalid[rb] ? qi : q_lo)) * p.q_sn +
+          (int64_t)(h * g + row % g) * p.q_sh + 8 * half;
+#pragma unroll
+      for (int ks_ = 0; ks_ < C::KS; ++ks_) {
+        u32x4 z = {0u, 0u, 0u, 0u};
+        if (rvalid[rb]) z = *reinterpret_cast<const u32x4*>(qp + 16 * ks_);
+        qf[rb][ks_] = z;
+      }
+    }
+
+    f32x16 o[RB][C::DT];
+    float m[RB], l[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+      for (int dt = 0; dt < C::DT; ++dt) o[rb][dt] = f32x16{};
+      m[rb] = -INFINITY;
+      l[rb] = 0.f;
+    }
+
+    // Per-lane LDS byte offsets (swizzled) of the MFMA operand reads, fixed
+    // for the whole loop: K rows 32 mt + col, chunk 2 ks + half (mt adds
+    // 32 rows, which keeps the swizzle); V transpose reads at rows
+    // 16 st + 4 half + L/4 (+8), chunk 4 dt + 2 (qg & 1) + (L & 3) / 2.
+    int koff[C::KS];
+#pragma unroll
+    for (int ks_ = 0; ks_ < C::KS; ++ks_) koff[ks_] = lds_off<D>(col, 2 * ks_ + half);
+    const int L = lane & 15;
+    const int qg = lane >> 4;
+    int voff[C::DT][2];
+#pragma unroll
+    for (int dt = 0; dt < C::DT; ++dt)
+#pragma unroll
+      for (int hi = 0; hi < 2; ++hi)
+        voff[dt][hi] = C::TILEB +
+                       lds_off<D>(4 * half + (L >> 2) + 8 * hi,
+                                  4 * dt + 2 * (qg & 1) + ((L & 3) >> 1)) +
+                       8 * (L & 1);
+
+    HalfRegs<D, BF16, FP8, RB> kr, vr;  // e4m3 staging only
+    float ksc_l = 0.f, vsc_l = 0.f;     // e4m3 scales of the computed tile
+    int pid = fetch_page_ids(p, ind_lo, npages, 0, lane);
+    if (n_tiles > 0) {
       if constexpr (FP8) {
-        // per-page K scales differ inside the tile: scale before the max
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) s[rb][mt][i] *= ksc[2 * mt + (i >> 3)];
+        load_half<D, BF16, FP8, RB, false>(kr, p, h, pid, npages, last, 0, wave, lane);
+        load_half<D, BF16, FP8, RB, true>(vr, p, h, pid, npages, last, 0, wave, lane);
+      } else {
+        dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid, npages, last, 0, st0, wave, lane);
+        dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid, npages, last, 0, st0 + C::TILEB,
+                                             wave, lane);
       }
-      if (need_mask) {
-        const int rel = lim[rb] - tok0 - 4 * half;  // visible iff offset <= rel
-#pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            if (32 * mt + 8 * (i >> 2) + (i & 3) > rel) s[rb][mt][i] = -INFINITY;
+    }
+    int pid_next = fetch_page_ids(p, ind_lo, npages, 1, lane);
+
+    // Iteration t: (e4m3: convert and store tile t) -- barrier -- issue tile
+    // t + 1's loads into the other stage, interleaved with tile t's MFMAs.
+    auto step = [&](int t, uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+      if constexpr (FP8) {
+        store_half<D, BF16, FP8, RB>(kr, cur, wave, lane);
+        store_half<D, BF16, FP8, RB>(vr, cur + C::TILEB, wave, lane);
+        ksc_l = kr.sc;
+        vsc_l = vr.sc;
       }
-      float mx = -INFINITY;
+      // Every wave's direct-to-LDS loads of tile t are complete before any wave
+      // passes the barrier and reads them.  The barrier itself waits only for
+      // LDS operations (workgroup-scope release), so this wait is explicit
+      // rather than left to the compiler's alias tracking of the loads.
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      __syncthreads();
+      const bool more = t + 1 < n_tiles;
+      pid = pid_next;
+      pid_next = fetch_page_ids(p, ind_lo, npages, t + 2, lane);
+
+      // ---- S^T = K . Q^T
+      f32x16 s[RB][2];
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[rb][mt][i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float c = FP8 ? 1.f : p.scale_log2;  // > 0: max commutes with it
-      const float mxs = mx * c;
-      if (__builtin_amdgcn_ballot_w64(mxs > m[rb] + kRescaleSlack)) {
-        const float m_new = fmaxf(m[rb], mxs);
-        const float alpha =
-            m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[rb] - m_new);
-        l[rb] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < C::DT; ++dt) o[rb][dt] *= alpha;
-        m[rb] = m_new;
-      }
-      const float mu = m[rb] == -INFINITY ? 0.f : m[rb];
-      float rs = 0.f;
+      for (int rb = 0; rb < RB; ++rb) s[rb][0] = s[rb][1] = f32x16{};
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][mt][i], c, -mu));
-          s[rb][mt][i] = e;
-          rs += e;
-        }
-      }
-      l[rb] += rs;
-    }
-
-    // ---- O^T += V^T . P^T over 4 steps of 16 tokens
+        for (int ks_ = 0; ks_ < C::KS; ++ks_) {
+          const u32x4 a =
+              *reinterpret_cast<const u32x4*>(cur + 32 * mt * C::ROWB + koff[ks_]);
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      if (st == 1 && more) {
-        if constexpr (FP8) {
-          load_half<D, BF16, FP8, RB, true>(vr, p, h, pid, npages, last, t + 1, wave, lane);
-        } else {
-          dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid, npages, last, t + 1,
-                                               nxt + C::TILEB, wave, lane);
+          for (int rb = 0; rb < RB; ++rb) s[rb][mt] = mfma32<BF16>(a, qf[rb][ks_], s[rb][mt]);
+        }
+        if (mt == 0 && more) {
+          if constexpr (FP8) {
+            load_half<D, BF16, FP8, RB, false>(kr, p, h, pid, npages, last, t + 1, wave, lane);
+          } else {
+            dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid, npages, last, t + 1, nxt, wave,
+                                                  lane);
+          }
         }
       }
-      u32x4 pb[RB];
+
+      // ---- online softmax in log2 units; lane holds 32 of the tile's 64
+      // tokens of its row (token 32 mt + 8 (i/4) + 4 half + i%4 in register i)
+      const int tok0 = t * BN;
+      const bool need_mask = tok0 + BN > clean_end;
+      float ksc[4], vsc[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ksc[i] = FP8 ? lane_value(ksc_l, i) * p.scale_log2 : p.scale_log2;
+        vsc[i] = FP8 ? lane_value(vsc_l, i) : 1.f;
+      }
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
+        if constexpr (FP8) {
+          // per-page K scales differ inside the tile: scale before the max
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r0 = 8 * (st & 1) + 2 * i;
-          pb[rb][i] = pack2_16<BF16>(s[rb][st >> 1][r0] * vsc[st],
-                                     s[rb][st >> 1][r0 + 1] * vsc[st]);
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[rb][mt][i] *= ksc[2 * mt + (i >> 3)];
+        }
+        if (need_mask) {
+          const int rel = lim[rb] - tok0 - 4 * half;  // visible iff offset <= rel
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              if (32 * mt + 8 * (i >> 2) + (i & 3) > rel) s[rb][mt][i] = -INFINITY;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[rb][mt][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float c = FP8 ? 1.f : p.scale_log2;  // > 0: max commutes with it
+        const float mxs = mx * c;
+        if (__builtin_amdgcn_ballot_w64(mxs > m[rb] + kRescaleSlack)) {
+          const float m_new = fmaxf(m[rb], mxs);
+          const float alpha =
+              m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m[rb] - m_new);
+          l[rb] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < C::DT; ++dt) o[rb][dt] *= alpha;
+          m[rb] = m_new;
+        }
+        const float mu = m[rb] == -INFINITY ? 0.f : m[rb];
+        float rs = 0.f;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][mt][i], c, -mu));
+            s[rb][mt][i] = e;
+            rs += e;
+          }
+        }
+        l[rb] += rs;
+      }
+
+      // ---- O^T += V^T . P^T over 4 steps of 16 tokens
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        if (st == 1 && more) {
+          if constexpr (FP8) {
+            load_half<D, BF16, FP8, RB, true>(vr, p, h, pid, npages, last, t + 1, wave, lane);
+          } else {
+            dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid, npages, last, t + 1,
+                                                 nxt + C::TILEB, wave, lane);
+          }
+        }
+        u32x4 pb[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r0 = 8 * (st & 1) + 2 * i;
+            pb[rb][i] = pack2_16<BF16>(s[rb][st >> 1][r0] * vsc[st],
+                                       s[rb][st >> 1][r0 + 1] * vsc[st]);
+          }
+        }
+#pragma unroll
+        for (int dt = 0; dt < C::DT; ++dt) {
+          const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_i16x4*)(cur + 16 * st * C::ROWB + voff[dt][0]));
+          const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_i16x4*)(cur + 16 * st * C::ROWB + voff[dt][1]));
+          const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
+          const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
+          const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
+#pragma unroll
+          for (int rb = 0; rb < RB; ++rb) o[rb][dt] = mfma32<BF16>(a, pb[rb], o[rb][dt]);
         }
       }
+    };
+    for (int t = 0; t < n_tiles; t += 2) {
+      step(t, st0, st1);
+      if (t + 1 >= n_tiles) break;
+      step(t + 1, st1, st0);
+    }
+
+    // ---- epilogue: O^T / l, lane's row, 4 consecutive d per register quad
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) {
+      const float l_tot = l[rb] + __shfl_xor(l[rb], 32);
+      if (!rvalid[rb]) continue;
+      const int row = 32 * (RB * wave + rb) + col;
+      const int qi = q_lo + row / g;
+      const int head = h * g + row % g;
+      const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+      uint16_t* orow = p.out + ((int64_t)(qo_start + qi) * p.hq + head) * D;
 #pragma unroll
       for (int dt = 0; dt < C::DT; ++dt) {
-        const i16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(cur + 16 * st * C::ROWB + voff[dt][0]));
-        const i16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (lds_i16x4*)(cur + 16 * st * C::ROWB + voff[dt][1]));
-        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
-        const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
-        const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
 #pragma unroll
-        for (int rb = 0; rb < RB; ++rb) o[rb][dt] = mfma32<BF16>(a, pb[rb], o[rb][dt]);
+        for (int i4 = 0; i4 < 4; ++i4) {
+          u32x2 w;
+          w[0] = pack2_16<BF16>(o[rb][dt][4 * i4] * inv, o[rb][dt][4 * i4 + 1] * inv);
+          w[1] = pack2_16<BF16>(o[rb][dt][4 * i4 + 2] * inv, o[rb][dt][4 * i4 + 3] * inv);
+          *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * half) = w;
+        }
       }
+      if (p.lse && half == 0)
+        p.lse[(int64_t)(qo_start + qi) * p.hq + head] =
+            l_tot > 0.f ? (m[rb] + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
     }
-  };
-  for (int t = 0; t < n_tiles; t += 2) {
-    step(t, st0, st1);
-    if (t + 1 >= n_tiles) break;
-    step(t + 1, st1, st0);
-  }
-
-  // ---- epilogue: O^T / l, lane's row, 4 consecutive d per register quad
-#pragma unroll
-  for (int rb = 0; rb < RB; ++rb) {
-    const float l_tot = l[rb] + __shfl_xor(l[rb], 32);
-    if (!rvalid[rb]) continue;
-    const int row = 32 * (RB * wave + rb) + col;
-    const int qi = q_lo + row / g;
-    const int head = h * g + row % g;
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    uint16_t* orow = p.out + ((int64_t)(qo_start + qi) * p.hq + head) * D;
-#pragma unroll
-    for (int dt = 0; dt < C::DT; ++dt) {
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        u32x2 w;
-        w[0] = pack2_16<BF16>(o[rb][dt][4 * i4] * inv, o[rb][dt][4 * i4 + 1] * inv);
-        w[1] = pack2_16<BF16>(o[rb][dt][4 * i4 + 2] * inv, o[rb][dt][4 * i4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4 + 4 * half) = w;
-      }
-    }
-    if (p.lse && half == 0)
-      p.lse[(int64_t)(qo_start + qi) * p.hq + head] =
-          l_tot > 0.f ? (m[rb] + log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
-  }
   };
 
   if constexpr (PAIRS) {
