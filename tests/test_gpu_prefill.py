@@ -30,7 +30,7 @@ EDGE = [(0, 1), (0, 15), (0, 16), (0, 17), (16, 1), (5, 33), (100, 64), (0, 130)
 
 
 @pytest.mark.parametrize("d", [64, 128])
-@pytest.mark.parametrize("hq,hkv", [(32, 8), (32, 4), (8, 8), (64, 8), (32, 2)])
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (32, 4), (8, 8), (64, 8), (32, 2), (12, 3)])
 @pytest.mark.parametrize("causal", [True, False])
 def test_prefill_edges(gpu, d, hq, hkv, causal):
     computed = [c for c, _ in EDGE]
