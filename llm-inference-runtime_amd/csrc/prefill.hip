@@ -25,6 +25,7 @@
 // zero without touching memory.  Causal tiles entirely below the diagonal
 // skip masking; tiles above the last row's diagonal are never visited.
 #include <algorithm>
+#include <cfloat>
 #include <climits>
 #include <cmath>
 #include <cstdlib>
@@ -452,18 +453,11 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       float ksc[4], vsc[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        ksc[i] = FP8 ? lane_value(ksc_l, i) * p.scale_log2 : p.scale_log2;
+        ksc[i] = FP8 ? fmaxf(lane_value(ksc_l, i) * p.scale_log2, FLT_MIN) : p.scale_log2;
         vsc[i] = FP8 ? lane_value(vsc_l, i) : 1.f;
       }
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        if constexpr (FP8) {
-          // per-page K scales differ inside the tile: scale before the max
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s[rb][mt][i] *= ksc[2 * mt + (i >> 3)];
-        }
         if (need_mask) {
           const int rel = lim[rb] - tok0 - 4 * half;  // visible iff offset <= rel
 #pragma unroll
@@ -472,14 +466,26 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
             for (int i = 0; i < 16; ++i)
               if (32 * mt + 8 * (i >> 2) + (i & 3) > rel) s[rb][mt][i] = -INFINITY;
         }
-        float mx = -INFINITY;
+        // e4m3: the page scale (> 0; FLT_MIN stands in for an empty page,
+        // whose K rows are zero) multiplies each page's max once and enters
+        // the exponent's FMA, since max commutes with a positive factor
+        float mxs = -INFINITY;
+        if constexpr (FP8) {
 #pragma unroll
-        for (int mt = 0; mt < 2; ++mt)
+          for (int q = 0; q < 4; ++q) {
+            float pm = -INFINITY;
 #pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[rb][mt][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float c = FP8 ? 1.f : p.scale_log2;  // > 0: max commutes with it
-        const float mxs = mx * c;
+            for (int i = 0; i < 8; ++i) pm = fmaxf(pm, s[rb][q >> 1][8 * (q & 1) + i]);
+            mxs = fmaxf(mxs, pm * ksc[q]);
+          }
+        } else {
+#pragma unroll
+          for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mxs = fmaxf(mxs, s[rb][mt][i]);
+          mxs *= p.scale_log2;  // > 0: max commutes with it
+        }
+        mxs = fmaxf(mxs, __shfl_xor(mxs, 32));
         if (__builtin_amdgcn_ballot_w64(mxs > m[rb] + kRescaleSlack)) {
           const float m_new = fmaxf(m[rb], mxs);
           const float alpha =
@@ -495,6 +501,7 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
         for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
+            const float c = FP8 ? ksc[2 * mt + (i >> 3)] : p.scale_log2;
             const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rb][mt][i], c, -mu));
             s[rb][mt][i] = e;
             rs += e;
