@@ -447,8 +447,11 @@ def rope(x: torch.Tensor, pos, theta: float, scale: float = 1.0, rotary_dim: int
     x [N, H, D] (fp32 result): angle_i = (pos / scale) * theta^(-2i/rotary_dim),
     rotate-half pairs (i, i + rotary_dim/2) or interleaved pairs (2i, 2i+1).
     Angles are formed in fp64.  Pinned by: test_rope_matches_transformers
-    (transformers' rotate_half / apply_rotary_pos_emb, modeling_llama.py) and
-    test_rope_is_rotation (norm preserved, pos 0 is the identity)."""
+    (transformers' rotate_half / apply_rotary_pos_emb, modeling_llama.py),
+    test_rope_is_rotation (norm preserved, pos 0 is the identity) and, for the
+    interleaved pairs, test_rope_interleave_closed_form (rotate-half RoPE of
+    the de-interleaved vector, re-interleaved; a planted -angle rotation and
+    planted rotate-half pairs fail it)."""
     n, h, d = x.shape
     rd = rotary_dim or d
     half = rd // 2

@@ -538,6 +538,55 @@ def test_rope_is_rotation():
     assert torch.equal(y[..., 8:], x[..., 8:])
 
 
+def _rope_interleaved_via_rotate_half(x, pos, theta, scale=1.0, rotary_dim=None):
+    """Interleaved RoPE (pairs 2i, 2i+1) written as rotate-half RoPE (pairs i,
+    i + rd/2) of the de-interleaved vector: gather the rotary dims in the order
+    0, 2, 4, ..., 1, 3, 5, ..., rotate, and scatter them back."""
+    rd = rotary_dim or x.shape[-1]
+    perm = torch.cat([torch.arange(0, rd, 2), torch.arange(1, rd, 2)])
+    xd = x.clone()
+    xd[..., :rd] = x[..., perm]
+    yd = O.rope(xd, pos, theta, scale=scale, rotary_dim=rd)
+    y = yd.clone()
+    y[..., perm] = yd[..., :rd]
+    return y
+
+
+def _rope_interleaved_negative_angle(x, pos, theta):
+    """A plausible mistake: the interleaved pairs rotated by -angle (the sign
+    of sin flipped)."""
+    d = x.shape[-1]
+    i = torch.arange(d // 2, dtype=torch.float64)
+    ang = torch.as_tensor(np.asarray(pos), dtype=torch.float64)[:, None] * theta ** (-(2.0 * i) / d)
+    c, s = torch.cos(ang).float()[:, None, :], torch.sin(ang).float()[:, None, :]
+    a, b = x[..., 0::2].float(), x[..., 1::2].float()
+    y = x.float().clone()
+    y[..., 0::2] = a * c + b * s
+    y[..., 1::2] = b * c - a * s
+    return y
+
+
+def test_rope_interleave_closed_form():
+    # the rotate-half form is pinned against transformers above; the
+    # interleaved form must equal it on the de-interleaved vector, for full and
+    # partial rotary dims and with linear position scaling
+    x = torch.randn(33, 3, 64)
+    pos = np.random.default_rng(5).integers(0, 131072, 33)
+    for rd, scale in ((None, 1.0), (32, 1.0), (None, 8.0)):
+        got = O.rope(x, pos, 500000.0, scale=scale, rotary_dim=rd, interleave=True)
+        want = _rope_interleaved_via_rotate_half(x, pos, 500000.0, scale=scale, rotary_dim=rd)
+        assert torch.allclose(got, want, atol=1e-6), (rd, scale)
+    # planted: a rotation by -angle keeps the norm and the position-0 identity
+    # (what test_rope_is_rotation checks) but fails the closed form
+    bad = _rope_interleaved_negative_angle(x, pos, 500000.0)
+    assert torch.allclose(bad.norm(dim=-1), x.norm(dim=-1), atol=1e-4)
+    assert not torch.allclose(bad, _rope_interleaved_via_rotate_half(x, pos, 500000.0), atol=1e-3)
+    # planted: pairs (i, i + D/2) instead of (2i, 2i+1) also fails it
+    wrong_pairs = O.rope(x, pos, 500000.0, interleave=False)
+    assert not torch.allclose(wrong_pairs, _rope_interleaved_via_rotate_half(x, pos, 500000.0),
+                              atol=1e-3)
+
+
 # -----------------------------------------------------------------------------
 # planted mistakes: each plausible bug in a copy of the oracle fails a pin
 
