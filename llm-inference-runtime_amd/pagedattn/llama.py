@@ -134,26 +134,41 @@ def plan_prefill(*, qo_indptr: torch.Tensor, kv_indptr: torch.Tensor, kv_indices
 def plan_decode(*, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
                 kv_last_page_len: torch.Tensor, num_qo_heads: int, num_kv_heads: int,
                 head_dim: int) -> None:
-    """(src/models/llama.py:119-147)"""
+    """(src/models/llama.py:119-147).  The planner needs kv_indptr and
+    kv_last_page_len on the host; batch_indices travels in the same
+    device-to-host copy, so the check for the fused decode rows costs no
+    transfer of its own."""
     FlashInferState.mode = "decode"
     FlashInferState.kv_indptr = kv_indptr
     FlashInferState.kv_indices = kv_indices
     FlashInferState.kv_last_page_len = kv_last_page_len
+    bsz = kv_last_page_len.numel()
+    bi = FlashInferState.batch_indices
+    check = (bi is not None and bi.numel() == bsz and bi.device == kv_indptr.device
+             and kv_last_page_len.device == kv_indptr.device)
+    parts = [kv_indptr.reshape(-1).to(torch.int32), kv_last_page_len.reshape(-1).to(torch.int32)]
+    if check:
+        parts.append(cast(torch.Tensor, bi).detach().reshape(-1).to(torch.int32))
+    if kv_last_page_len.device == kv_indptr.device:
+        host = torch.cat(parts).cpu()
+    else:
+        host = torch.cat([p.cpu() for p in parts])
+    n_ptr = kv_indptr.numel()
+    indptr_h, last_h = host[:n_ptr], host[n_ptr:n_ptr + bsz]
     dw = cast(ops.BatchDecodeWithPagedKVCacheWrapper, FlashInferState.decode_wrapper)
     dw.begin_forward(kv_indptr, kv_indices, kv_last_page_len, num_qo_heads, num_kv_heads,
-                     head_dim, FlashInferState.page_size, q_data_type=_q_dtype())
-    FlashInferState._fused_rows = _identity_rows(FlashInferState.batch_indices,
-                                                 kv_last_page_len.numel())
+                     head_dim, FlashInferState.page_size, q_data_type=_q_dtype(),
+                     indptr_host=indptr_h.reshape(kv_indptr.shape),
+                     last_page_len_host=last_h.reshape(kv_last_page_len.shape))
+    FlashInferState._fused_rows = (
+        _identity_rows(cast(torch.Tensor, bi), host[n_ptr + bsz:]) if check else None)
 
 
-def _identity_rows(batch_indices: torch.Tensor | None, bsz: int) -> tuple | None:
-    """(batch_indices, its in-place version) when it is arange(bsz), the
-    engine's decode rows (step_executor.py:220-222), else None.  Reads the
-    tensor on the host: the plan already waits for its metadata copy."""
-    if batch_indices is None or batch_indices.numel() != bsz:
-        return None
-    got = batch_indices.detach().to("cpu", torch.int64)
-    if not torch.equal(got, torch.arange(bsz, dtype=torch.int64)):
+def _identity_rows(batch_indices: torch.Tensor, host_rows: torch.Tensor) -> tuple | None:
+    """(batch_indices, its in-place version) when its host copy `host_rows`
+    is arange(B), the engine's decode rows (step_executor.py:220-222), else
+    None."""
+    if not torch.equal(host_rows.to(torch.int64), torch.arange(host_rows.numel(), dtype=torch.int64)):
         return None
     return batch_indices, batch_indices._version
 

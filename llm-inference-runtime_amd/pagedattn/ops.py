@@ -569,7 +569,12 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
              logits_soft_cap: float | None = None, q_data_type="float16",
              kv_data_type=None, data_type=None, sm_scale: float | None = None,
              rope_scale=None, rope_theta=None, non_blocking: bool = True,
-             split_pages: int = 0, device_plan: bool = False, **_unused) -> None:
+             split_pages: int = 0, device_plan: bool = False,
+             indptr_host: torch.Tensor | None = None,
+             last_page_len_host: torch.Tensor | None = None, **_unused) -> None:
+        """indptr_host / last_page_len_host: CPU copies of indptr and
+        last_page_len that the caller already holds; the plan then makes no
+        device-to-host copy of its own."""
         _unsupported_options(pos_encoding_mode, window_left, logits_soft_cap)
         if page_size != PAGE_SIZE:
             raise NotImplementedError(f"page_size {page_size} (only 16 is implemented)")
@@ -579,8 +584,12 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
                               sm_scale)
             return
         device = self._ws.device
-        indptr_h = _host_i32(indptr)
-        last_h = _host_i32(last_page_len)
+        indptr_h = _host_i32(indptr if indptr_host is None else indptr_host)
+        last_h = _host_i32(last_page_len if last_page_len_host is None else last_page_len_host)
+        if indptr_host is not None and indptr_h.shape != indptr.shape:
+            raise ValueError("indptr_host must have indptr's shape")
+        if last_page_len_host is not None and last_h.shape != last_page_len.shape:
+            raise ValueError("last_page_len_host must have last_page_len's shape")
         bsz = last_h.numel()
         if indptr_h.numel() != bsz + 1:
             raise ValueError(f"indptr has {indptr_h.numel()} entries for {bsz} sequences")

@@ -147,6 +147,38 @@ def test_fused_decode_needs_identity_rows(gpu):
     assert not torch.equal(ident[3], fused[3])
 
 
+def test_plan_decode_one_host_copy(gpu):
+    """plan_decode brings kv_indptr, kv_last_page_len and batch_indices to the
+    host in one device-to-host copy (the planner needs the first two; the
+    third decides whether the fused decode launch applies): torch's sync
+    debug mode sees exactly one synchronising operation, and the fused rows
+    are still recognised (and rejected for a permutation)."""
+    import warnings
+    L.init_flashinfer_state(kv_pool=torch.zeros((1, 64, 2, 2, 16, 64), dtype=torch.bfloat16,
+                                                device=gpu), page_size=16, device=gpu)
+    rng = np.random.default_rng(3)
+    lens = [37, 100, 5, 64]
+    tables, _ = random_tables(rng, lens, extra_pages=4)
+    meta = decode_metadata(tables, lens)
+    args = dict(kv_indptr=i32(meta.kv_indptr, gpu), kv_indices=i32(meta.kv_indices, gpu),
+                kv_last_page_len=i32(meta.kv_last_page_len, gpu), num_qo_heads=8,
+                num_kv_heads=2, head_dim=64)
+    for rows, fused in ((np.arange(4), True), (np.array([2, 0, 3, 1]), False)):
+        L.FlashInferState.batch_indices = i32(rows.astype(np.int32), gpu)
+        torch.cuda.synchronize()
+        prev = torch.cuda.get_sync_debug_mode()
+        torch.cuda.set_sync_debug_mode("warn")
+        try:
+            with warnings.catch_warnings(record=True) as caught:
+                warnings.simplefilter("always")
+                L.plan_decode(**args)
+        finally:
+            torch.cuda.set_sync_debug_mode(prev)
+        syncs = [w for w in caught if "synchroniz" in str(w.message)]
+        assert len(syncs) == 1, [str(w.message) for w in syncs]
+        assert (L.FlashInferState._fused_rows is not None) == fused
+
+
 # -----------------------------------------------------------------------------
 # "Option A" of the integration: the engine keeps its own attention shim and
 # imports this package under FlashInfer's name.  The forward and state set-up
