@@ -754,17 +754,11 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
 // writes the output.  No sequence is
 // cut across workgroups, so there are no split partials and no merge launch.
 
-constexpr int kSharedMaxItems = 8;  // items per workgroup (the planner's bound)
 constexpr int kSharedSlots = 2;     // items whose states can wait in LDS at once
-constexpr int kSharedStagePairs = 1;  // page pairs per chunk (register stage)
 // Bound of the wait for a slot to be released (each round sleeps ~64 clocks);
 // the wait always ends long before, since a slot only waits for items of
 // lower index, whose waves never wait for it.
 constexpr int kSharedSpinLimit = 1 << 24;
-
-struct SharedItem {
-  int32_t b, h, chunk_lo, n_chunks;
-};
 
 template <int D>
 struct SharedLds {
@@ -1241,468 +1235,10 @@ static DecodeFn pick_decode(int d, bool bf16, bool fp8, bool append, bool rope, 
                   : decode_fn_d<128, false>(bf16, fp8, append, rope);
 }
 
-// Waves the planner spreads the work over, per CU (one wave per SIMD keeps
-// enough loads in flight with two register stages);
-// PAGEDATTN_DECODE_WAVES_PER_CU overrides it.
-static int decode_waves_per_cu() {
-  if (const char* env = std::getenv("PAGEDATTN_DECODE_WAVES_PER_CU")) {
-    const int v = std::atoi(env);
-    if (v > 0) return v;
-  }
-  return 4;
-}
-
-// Page-equivalents charged per item by the balanced split (the cost of an
-// item switch, measured: 6 gave the fastest TinyLlama B=256 step, 60.5 us
-// against 63.7 us at 0); PAGEDATTN_DECODE_ITEM_COST overrides it.
-static int decode_item_cost() {
-  if (const char* env = std::getenv("PAGEDATTN_DECODE_ITEM_COST")) {
-    const int v = std::atoi(env);
-    if (v >= 0 && v <= 1024) return v;
-  }
-  return 6;
-}
-
-// Waves (KV heads) per head group: the largest of 4, 2, 1 that divides Hkv,
-// so a page's K and V blocks are each read as one run of hg * 16 rows;
-// PAGEDATTN_DECODE_HEAD_GROUP (1, 2 or 4) caps it.
-static int decode_head_group(int hkv) {
-  int cap = 4;
-  if (const char* env = std::getenv("PAGEDATTN_DECODE_HEAD_GROUP")) {
-    const int v = std::atoi(env);
-    if (v == 1 || v == 2 || v == 4) cap = v;
-  }
-  int hg = 1;
-  while (hg * 2 <= cap && hkv % (hg * 2) == 0) hg *= 2;
-  return hg;
-}
-
-// Shared-item plans (decode_shared_kernel): PAGEDATTN_DECODE_SHARED=0 turns
-// them off, =1 takes one whenever the items fit a workgroup's table; by
-// default one is taken when its busiest CU holds at most
-// PAGEDATTN_DECODE_SHARED_SLACK_KB KiB more K/V than the mean (default 96:
-// what one CU streams in about the 4-5 us that the split's merge launch
-// costs).
-static int decode_shared_mode() {
-  if (const char* env = std::getenv("PAGEDATTN_DECODE_SHARED")) {
-    const int v = std::atoi(env);
-    if (v == 0 || v == 1) return v;
-  }
-  return -1;
-}
-// Shared plans claim chunks in arrival order (fastest);
-// PAGEDATTN_DECODE_DETERMINISTIC=1 gives them a fixed chunk assignment,
-// whose output bits do not depend on timing.
-static bool decode_deterministic() {
-  const char* env = std::getenv("PAGEDATTN_DECODE_DETERMINISTIC");
-  return env && std::atoi(env) == 1;
-}
-
-static int64_t decode_shared_slack_bytes() {
-  if (const char* env = std::getenv("PAGEDATTN_DECODE_SHARED_SLACK_KB")) {
-    const int v = std::atoi(env);
-    if (v >= 0) return (int64_t)v << 10;
-  }
-  return (int64_t)96 << 10;
-}
-
-// Shared-item partition: whole (sequence, KV head) items, longest first onto
-// the least-loaded of `cus` workgroups, in chunks of kSharedStagePairs page
-// pairs.  Returns false (and leaves the outputs unspecified) when some
-// workgroup would hold more than kSharedMaxItems items or, unless forced,
-// when the busiest workgroup exceeds the mean by more than the slack.
-static bool plan_shared(const std::vector<int32_t>& npages, int hkv, int d, int cus, bool forced,
-                        std::vector<SharedItem>* items, std::vector<int32_t>* wg_ptr) {
-  const int batch = (int)npages.size();
-  const int64_t n_all = (int64_t)batch * hkv;
-  // built for D = 64: at D = 128 two register stages, the merge and the
-  // output conversion do not fit the register file together
-  if (n_all == 0 || d != 64) return false;
-  const int chunk_pages = 2 * kSharedStagePairs;
-  std::vector<int32_t> order((size_t)n_all);
-  for (int64_t i = 0; i < n_all; ++i) order[(size_t)i] = (int32_t)i;
-  // sequence-major item ids; longest first, ties in id order
-  std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t c) {
-    return npages[a / hkv] > npages[c / hkv];
-  });
-  const int n_wg = (int)std::min<int64_t>(std::max(cus, 1), n_all);
-  std::vector<std::vector<int32_t>> per(n_wg);
-  std::vector<int64_t> load(n_wg, 0);
-  std::priority_queue<std::pair<int64_t, int>, std::vector<std::pair<int64_t, int>>,
-                      std::greater<std::pair<int64_t, int>>> heap;
-  for (int w = 0; w < n_wg; ++w) heap.push({0, w});
-  for (int32_t id : order) {
-    auto top = heap.top();
-    heap.pop();
-    per[top.second].push_back(id);
-    // a chunk streams its pages; an empty item still costs one chunk's visit
-    top.first += std::max(1, npages[id / hkv]);
-    load[top.second] = top.first;
-    heap.push(top);
-  }
-  int64_t sum = 0, mx = 0;
-  for (int w = 0; w < n_wg; ++w) {
-    if ((int)per[w].size() > kSharedMaxItems) return false;
-    sum += load[w];
-    mx = std::max(mx, load[w]);
-  }
-  // K and V of one page of one KV head, counted at 16 bits per element
-  const int64_t page_bytes = (int64_t)kPage * d * 2 * 2;
-  if (!forced && (mx * n_wg - sum) * page_bytes > decode_shared_slack_bytes() * n_wg) return false;
-  items->clear();
-  wg_ptr->assign(1, 0);
-  for (int w = 0; w < n_wg; ++w) {
-    int32_t chunk = 0;
-    for (int32_t id : per[w]) {
-      const int32_t np = npages[id / hkv];
-      const int32_t nc = std::max<int32_t>(1, ((np + 1) / 2 + chunk_pages / 2 - 1) / (chunk_pages / 2));
-      items->push_back(SharedItem{id / hkv, id % hkv, chunk, nc});
-      chunk += nc;
-    }
-    wg_ptr->push_back((int32_t)items->size());
-  }
-  return true;
-}
-
-// The device-side partition of a decode plan (pagedattn_decode_plan_device
-// and pagedattn_decode_run_noalloc): shares of the (sequence, head group,
-// page) stream for cus x waves-per-CU / hg head groups, split partials at
-// `partials` (256-byte aligned, `bytes` long).
-static int setup_device_plan(const char* who, pagedattn_plan* plan, int32_t batch_size,
-                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
-                             int32_t page_size, int cus, char* partials, size_t bytes) {
-  plan->mode = kPlanNone;
-  if (batch_size < 0)
-    return set_error(PAGEDATTN_ERR_INVALID, "%s: batch_size %d < 0", who, batch_size);
-  int rc = validate_heads(who, num_qo_heads, num_kv_heads, head_dim, page_size);
-  if (rc) return rc;
-  const int hg = decode_head_group(num_kv_heads);
-  const int g = num_qo_heads / num_kv_heads;
-  const int n_groups = std::max(1, cus * decode_waves_per_cu() / hg);
-  const int n_slots = 2 * n_groups * hg;
-  const size_t off_pl = ws_align(sizeof(float) * (size_t)n_slots * g * head_dim);
-  const size_t end = ws_align(off_pl + sizeof(float) * (size_t)n_slots * g);
-  if (end > bytes)
-    return set_error(PAGEDATTN_ERR_WORKSPACE, "%s: needs %zu bytes of split partials, %zu "
-                     "available", who, end, bytes);
-  plan->implicit = true;
-  plan->shared = false;
-  plan->item_cost = decode_item_cost();
-  plan->batch_size = batch_size;
-  plan->hq = num_qo_heads;
-  plan->hkv = num_kv_heads;
-  plan->d = head_dim;
-  plan->page_size = page_size;
-  plan->n_items = n_groups;
-  plan->hg_shift = hg == 4 ? 2 : hg == 2 ? 1 : 0;
-  plan->n_merge = 0;
-  plan->n_slots = n_slots;
-  plan->split_pages = 0;
-  plan->items_dev = nullptr;
-  plan->wave_ptr_dev = nullptr;
-  plan->merge_dev = nullptr;
-  plan->partial_o = reinterpret_cast<float*>(partials);
-  plan->partial_lse = reinterpret_cast<float*>(partials + off_pl);
-  plan->total_pages = -1;
-  plan->max_pages = -1;
-  plan->mode = kPlanDecode;
-  return PAGEDATTN_OK;
-}
-
 }  // namespace pa
 
 using namespace pa;
 
-extern "C" {
-
-int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
-                          const int32_t* kv_last_page_len_host,
-                          int32_t batch_size, int32_t num_qo_heads,
-                          int32_t num_kv_heads, int32_t head_dim,
-                          int32_t page_size, int32_t split_pages,
-                          void* workspace, size_t workspace_bytes,
-                          void* stream) {
-  const char* who = "decode_plan";
-  if (!plan) return set_error(PAGEDATTN_ERR_INVALID, "%s: null plan", who);
-  plan->mode = kPlanNone;
-  if (batch_size < 0)
-    return set_error(PAGEDATTN_ERR_INVALID, "%s: batch_size %d < 0", who,
-                     batch_size);
-  int rc = validate_heads(who, num_qo_heads, num_kv_heads, head_dim, page_size);
-  if (rc) return rc;
-  if (!workspace || ((uintptr_t)workspace & (kWsAlign - 1)))
-    return set_error(PAGEDATTN_ERR_INVALID,
-                     "%s: workspace must be a 256-byte aligned device buffer",
-                     who);
-  std::vector<int32_t> npages, kv_len;
-  rc = validate_paged_metadata(who, kv_indptr_host, kv_last_page_len_host,
-                               batch_size, page_size, &npages, &kv_len);
-  if (rc) return rc;
-  const int hkv = num_kv_heads;
-  const int g = num_qo_heads / num_kv_heads;
-
-  int64_t total = 0;
-  int maxp = 0;
-  for (int b = 0; b < batch_size; ++b) {
-    total += npages[b];
-    maxp = std::max(maxp, npages[b]);
-  }
-  int cus = device_cu_count();
-  if (cus <= 0) cus = 256;
-  plan->shared = false;
-
-  if (split_pages == 0 && decode_shared_mode() != 0) {
-    std::vector<SharedItem> sitems;
-    std::vector<int32_t> wg_ptr;
-    if (plan_shared(npages, hkv, head_dim, cus, decode_shared_mode() == 1, &sitems, &wg_ptr)) {
-      const int n_wg = (int)wg_ptr.size() - 1;
-      const size_t off_items = kWsHeader;
-      const size_t off_wg = ws_align(off_items + sizeof(SharedItem) * sitems.size());
-      const size_t end = ws_align(off_wg + sizeof(int32_t) * wg_ptr.size());
-      const size_t host_bytes = end - kWsHeader;
-      plan->host.assign(host_bytes / sizeof(int32_t), 0);
-      char* hb = reinterpret_cast<char*>(plan->host.data());
-      std::memcpy(hb, sitems.data(), sizeof(SharedItem) * sitems.size());
-      std::memcpy(hb + (off_wg - kWsHeader), wg_ptr.data(), sizeof(int32_t) * wg_ptr.size());
-      plan->workspace = workspace;
-      plan->workspace_bytes = workspace_bytes;
-      rc = upload_plan(plan, who, host_bytes, end, stream);
-      if (rc) return rc;
-      char* ws = static_cast<char*>(workspace);
-      plan->implicit = false;
-      plan->shared = true;
-      plan->deterministic = decode_deterministic();
-      plan->batch_size = batch_size;
-      plan->hq = num_qo_heads;
-      plan->hkv = num_kv_heads;
-      plan->d = head_dim;
-      plan->page_size = page_size;
-      plan->n_items = n_wg;
-      plan->hg_shift = 0;
-      plan->n_merge = 0;
-      plan->n_slots = 0;
-      plan->split_pages = split_pages;
-      plan->items_dev = ws + off_items;
-      plan->wave_ptr_dev = reinterpret_cast<const int32_t*>(ws + off_wg);
-      plan->merge_dev = nullptr;
-      plan->partial_o = nullptr;
-      plan->partial_lse = nullptr;
-      plan->total_pages = total;
-      plan->max_pages = maxp;
-      plan->mode = kPlanDecode;
-      return PAGEDATTN_OK;
-    }
-  }
-
-  // work is planned per head group: hg KV heads walked together by hg waves
-  const int hg = decode_head_group(hkv);
-  const int hg_shift = hg == 4 ? 2 : hg == 2 ? 1 : 0;
-  const int ngrp = hkv / hg;  // head groups per sequence
-  const int64_t groups_max =
-      std::max<int64_t>(1, (int64_t)cus * decode_waves_per_cu() / hg);
-
-  // items, grouped per head group
-  std::vector<DecodeItem> items;
-  std::vector<int32_t> wave_ptr(1, 0);
-  std::vector<int32_t> pieces((size_t)batch_size * ngrp, 0);
-  auto make = [hg](int b, int hgrp, int lo, int hi) {
-    return DecodeItem{b, hgrp * hg, lo, hi, -1, -1, 0, 0};
-  };
-  if (split_pages != 0) {
-    // fixed chunks (split_pages > 0) or whole sequences (< 0), assigned
-    // longest-first onto the least-loaded head group
-    const int chunk = split_pages > 0 ? ((split_pages + 7) / 8) * 8 : INT32_MAX;
-    std::vector<DecodeItem> all;
-    for (int b = 0; b < batch_size; ++b)
-      for (int hgrp = 0; hgrp < ngrp; ++hgrp) {
-        if (npages[b] == 0) {
-          all.push_back(make(b, hgrp, 0, 0));
-          pieces[(size_t)b * ngrp + hgrp]++;
-          continue;
-        }
-        for (int lo = 0; lo < npages[b]; lo += chunk) {
-          all.push_back(make(b, hgrp, lo, (int)std::min<int64_t>(npages[b], (int64_t)lo + chunk)));
-          pieces[(size_t)b * ngrp + hgrp]++;
-        }
-      }
-    std::stable_sort(all.begin(), all.end(), [](const DecodeItem& a, const DecodeItem& c) {
-      return a.page_hi - a.page_lo > c.page_hi - c.page_lo;
-    });
-    const int64_t nw = std::min<int64_t>(groups_max, std::max<size_t>(1, all.size()));
-    std::vector<std::vector<int>> per_group(nw);
-    std::priority_queue<std::pair<int64_t, int64_t>,
-                        std::vector<std::pair<int64_t, int64_t>>,
-                        std::greater<std::pair<int64_t, int64_t>>> heap;
-    for (int64_t w = 0; w < nw; ++w) heap.push({0, w});
-    for (size_t i = 0; i < all.size(); ++i) {
-      auto top = heap.top();
-      heap.pop();
-      per_group[top.second].push_back((int)i);
-      top.first += std::max(1, all[i].page_hi - all[i].page_lo);
-      heap.push(top);
-    }
-    for (auto& lst : per_group) {
-      for (int i : lst) items.push_back(all[i]);
-      wave_ptr.push_back((int32_t)items.size());
-    }
-  } else {
-    // balanced: the (sequence, head group, page) stream cut into equal
-    // shares.  A share is counted in pages plus `cost` page-equivalents per
-    // item it holds, since every item start waits for a fresh round trip of
-    // loads: a share of several short pieces gets fewer pages and the groups
-    // finish together.  Shares are contiguous, so only a group's first and
-    // last items can be pieces of cut sequences.
-    const int64_t cost = decode_item_cost();
-    const int64_t est_items = (int64_t)batch_size * ngrp + groups_max;
-    int64_t target = (total * ngrp + cost * est_items + groups_max - 1) / groups_max;
-    target = std::max<int64_t>(4 + cost, (target + 1) / 2 * 2);
-    for (;;) {
-      items.clear();
-      wave_ptr.assign(1, 0);
-      std::fill(pieces.begin(), pieces.end(), 0);
-      int64_t fill = 0;
-      for (int b = 0; b < batch_size; ++b)
-        for (int hgrp = 0; hgrp < ngrp; ++hgrp) {
-          if (npages[b] == 0) {
-            items.push_back(make(b, hgrp, 0, 0));
-            pieces[(size_t)b * ngrp + hgrp]++;
-            continue;
-          }
-          int lo = 0;
-          while (lo < npages[b]) {
-            if (fill > 0 && fill + cost >= target) {
-              wave_ptr.push_back((int32_t)items.size());
-              fill = 0;
-            }
-            const int take = (int)std::min<int64_t>(npages[b] - lo, target - fill - cost);
-            items.push_back(make(b, hgrp, lo, lo + take));
-            pieces[(size_t)b * ngrp + hgrp]++;
-            lo += take;
-            fill += take + cost;
-            if (fill >= target) {
-              wave_ptr.push_back((int32_t)items.size());
-              fill = 0;
-            }
-          }
-        }
-      if (wave_ptr.back() != (int32_t)items.size())
-        wave_ptr.push_back((int32_t)items.size());
-      // the item charge can overshoot the estimate: never more shares than
-      // head groups the launch keeps resident
-      if ((int64_t)wave_ptr.size() - 1 <= groups_max || cost == 0) break;
-      target += 2;
-    }
-  }
-
-  // Partial slots and merge groups for (sequence, head group) pairs cut in
-  // pieces: piece k of head h0 + i writes slot base + k * hg + i, and the
-  // merge of (b, h0 + i) reads slots base + i + k * hg.
-  std::vector<MergeItem> merges;
-  std::vector<int32_t> first_merge((size_t)batch_size * ngrp, -1);
-  std::vector<int32_t> base_slot((size_t)batch_size * ngrp, -1);
-  int n_slots = 0;
-  for (int b = 0; b < batch_size; ++b)
-    for (int hgrp = 0; hgrp < ngrp; ++hgrp) {
-      const int np = pieces[(size_t)b * ngrp + hgrp];
-      if (np > 1) {
-        first_merge[(size_t)b * ngrp + hgrp] = (int)merges.size();
-        base_slot[(size_t)b * ngrp + hgrp] = n_slots;
-        for (int i = 0; i < hg; ++i)
-          merges.push_back(MergeItem{b, hgrp * hg + i, n_slots + i, np, hg});
-        n_slots += np * hg;
-      }
-    }
-  {
-    std::vector<int32_t> next((size_t)batch_size * ngrp, 0);
-    for (auto& it : items) {
-      const size_t key = (size_t)it.b * ngrp + it.h / hg;
-      if (first_merge[key] >= 0) {
-        it.merge = first_merge[key];
-        it.slot = base_slot[key] + hg * next[key]++;
-      }
-    }
-  }
-
-  const int n_items = (int)items.size();
-  const int n_waves = (int)wave_ptr.size() - 1;
-  const size_t n_merge = merges.size();
-  const size_t off_items = kWsHeader;
-  const size_t off_wave = ws_align(off_items + sizeof(DecodeItem) * n_items);
-  const size_t off_merge = ws_align(off_wave + sizeof(int32_t) * (n_waves + 1));
-  const size_t off_po = ws_align(off_merge + sizeof(MergeItem) * n_merge);
-  const size_t off_pl =
-      ws_align(off_po + sizeof(float) * (size_t)n_slots * g * head_dim);
-  const size_t end = ws_align(off_pl + sizeof(float) * (size_t)n_slots * g);
-  const size_t host_bytes = off_po - kWsHeader;
-
-  plan->host.assign(host_bytes / sizeof(int32_t), 0);
-  char* hb = reinterpret_cast<char*>(plan->host.data());
-  if (n_items)
-    std::memcpy(hb + (off_items - kWsHeader), items.data(), sizeof(DecodeItem) * n_items);
-  std::memcpy(hb + (off_wave - kWsHeader), wave_ptr.data(), sizeof(int32_t) * (n_waves + 1));
-  if (n_merge)
-    std::memcpy(hb + (off_merge - kWsHeader), merges.data(), sizeof(MergeItem) * n_merge);
-
-  plan->workspace = workspace;
-  plan->workspace_bytes = workspace_bytes;
-  rc = upload_plan(plan, who, host_bytes, end, stream);
-  if (rc) return rc;
-
-  char* ws = static_cast<char*>(workspace);
-  plan->implicit = false;
-  plan->batch_size = batch_size;
-  plan->hq = num_qo_heads;
-  plan->hkv = num_kv_heads;
-  plan->d = head_dim;
-  plan->page_size = page_size;
-  plan->n_items = n_waves;
-  plan->hg_shift = hg_shift;
-  plan->n_merge = (int)n_merge;
-  plan->n_slots = n_slots;
-  plan->split_pages = split_pages;
-  plan->items_dev = ws + off_items;
-  plan->wave_ptr_dev = reinterpret_cast<const int32_t*>(ws + off_wave);
-  plan->merge_dev = ws + off_merge;
-  plan->partial_o = reinterpret_cast<float*>(ws + off_po);
-  plan->partial_lse = reinterpret_cast<float*>(ws + off_pl);
-  plan->total_pages = total;
-  plan->max_pages = maxp;
-  plan->mode = kPlanDecode;
-  return PAGEDATTN_OK;
-}
-
-int pagedattn_decode_plan_kind(const pagedattn_plan* plan) {
-  if (!plan || plan->mode != kPlanDecode) return 0;
-  if (plan->implicit) return PAGEDATTN_DECODE_DEVICE;
-  return plan->shared ? PAGEDATTN_DECODE_SHARED : PAGEDATTN_DECODE_SPLIT;
-}
-
-int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
-                                 int32_t num_qo_heads, int32_t num_kv_heads,
-                                 int32_t head_dim, int32_t page_size, void* workspace,
-                                 size_t workspace_bytes) {
-  const char* who = "decode_plan_device";
-  if (!plan) return set_error(PAGEDATTN_ERR_INVALID, "%s: null plan", who);
-  plan->mode = kPlanNone;
-  if (!workspace || ((uintptr_t)workspace & (kWsAlign - 1)))
-    return set_error(PAGEDATTN_ERR_INVALID,
-                     "%s: workspace must be a 256-byte aligned device buffer", who);
-  int cus = device_cu_count();
-  if (cus <= 0) cus = 256;
-  if (workspace_bytes < kWsHeader)
-    return set_error(PAGEDATTN_ERR_WORKSPACE, "%s: workspace smaller than its %zu-byte header",
-                     who, kWsHeader);
-  plan->host.clear();
-  const int rc = setup_device_plan(who, plan, batch_size, num_qo_heads, num_kv_heads, head_dim,
-                                   page_size, cus, static_cast<char*>(workspace) + kWsHeader,
-                                   workspace_bytes - kWsHeader);
-  if (rc) return rc;
-  plan->workspace = workspace;
-  plan->workspace_bytes = workspace_bytes;
-  return PAGEDATTN_OK;
-}
-
-}  // extern "C"
 
 namespace pa {
 

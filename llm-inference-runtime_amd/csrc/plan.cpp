@@ -1,7 +1,7 @@
 // Host planner helpers: metadata validation and the upload of a work list
-// into the caller's workspace.  The decode / prefill partitioners themselves
-// live next to their kernels (decode.hip, prefill.hip) because they size the
-// partition from the kernels' occupancy.
+// into the caller's workspace.  The decode / prefill partitioners are in
+// decode_plan.cpp and prefill_plan.cpp.
+#include <climits>
 #include <cstring>
 
 #include "plan_internal.h"
@@ -31,8 +31,14 @@ int validate_paged_metadata(const char* who, const int32_t* kv_indptr_host,
       return set_error(PAGEDATTN_ERR_INVALID,
                        "%s: kv_last_page_len[%d] = %d outside [1, %d]", who, b,
                        last, page_size);
+    // kv lengths are int32 in the kernels
+    const int64_t len = np > 0 ? (int64_t)(np - 1) * page_size + last : 0;
+    if (len > INT32_MAX)
+      return set_error(PAGEDATTN_ERR_UNSUPPORTED,
+                       "%s: sequence %d holds %lld tokens (at most %d)", who, b,
+                       (long long)len, INT32_MAX);
     (*npages)[b] = np;
-    (*kv_len)[b] = np > 0 ? (np - 1) * page_size + last : 0;
+    (*kv_len)[b] = (int32_t)len;
   }
   return PAGEDATTN_OK;
 }

@@ -37,6 +37,26 @@ struct PrefillItem {
   int32_t b, q_lo, q_hi, slot;
 };
 
+// One item of a shared-item decode plan (decode_shared_kernel): sequence b,
+// KV head h, its page pairs being chunks [chunk_lo, chunk_lo + n_chunks) of
+// the workgroup's chunk sequence.
+struct SharedItem {
+  int32_t b, h, chunk_lo, n_chunks;
+};
+
+// Shared-item decode geometry the planner sizes its partition by: items per
+// workgroup (the kernel's LDS table) and page pairs per chunk (one register
+// stage).
+constexpr int kSharedMaxItems = 8;
+constexpr int kSharedStagePairs = 1;
+
+// Prefill geometry: 8 waves per workgroup (two per SIMD) share every K/V tile
+// loaded into LDS, which halves the global-to-LDS traffic per MFMA against 4
+// waves; each wave owns kPrefillRB blocks of 32 query rows.
+constexpr int kPrefillWaves = 8;
+constexpr int kPrefillRB = 1;
+constexpr int kPrefillRows = kPrefillWaves * 32 * kPrefillRB;
+
 // Workspace layout: [0, kWsHeader) is reserved for the caller's device flags
 // (the Python shim keeps the append error counter at offset 0).
 constexpr size_t kWsHeader = 256;

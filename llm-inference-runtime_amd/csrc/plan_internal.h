@@ -24,4 +24,12 @@ int validate_heads(const char* who, int32_t hq, int32_t hkv, int32_t d,
 int upload_plan(pagedattn_plan* plan, const char* who, size_t host_bytes,
                 size_t total_bytes, void* stream);
 
+// The device-side partition of a decode plan (pagedattn_decode_plan_device
+// and pagedattn_decode_run_noalloc): shares of the (sequence, head group,
+// page) stream for cus x waves-per-CU / hg head groups, split partials at
+// `partials` (256-byte aligned, `bytes` long).  Host only, allocates nothing.
+int setup_device_plan(const char* who, pagedattn_plan* plan, int32_t batch_size,
+                      int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                      int32_t page_size, int cus, char* partials, size_t bytes);
+
 }  // namespace pa
