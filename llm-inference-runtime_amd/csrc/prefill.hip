@@ -82,9 +82,6 @@ __device__ __forceinline__ uint32_t e4m3x2_to16(uint32_t w) {
   }
 }
 
-// Waves per workgroup: 8 (two per SIMD) share every K/V tile loaded into
-// LDS, which halves the global-to-LDS traffic per MFMA against 4 waves.
-constexpr int kPrefillWaves = 8;
 
 template <int D, bool BF16, bool FP8, int RB>
 struct PrefillCfg {
@@ -406,7 +403,13 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
 
     // Iteration t: (e4m3: convert and store tile t) -- barrier -- issue tile
     // t + 1's loads into the other stage, interleaved with tile t's MFMAs.
-    auto step = [&](int t, uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+    // The loads are issued on every tile (on the last one with no page, so
+    // they read nothing) and tiles that need no mask run a copy of the step
+    // without it: the step is then one branch-free block apart from the
+    // rare rescale, and the compiler can overlap its LDS reads, exps and
+    // MFMAs across the phases.
+    auto step = [&](auto mask_tag, int t, uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+      constexpr bool MASK = decltype(mask_tag)::value;
       if constexpr (FP8) {
         store_half<D, BF16, FP8, RB>(kr, cur, wave, lane);
         store_half<D, BF16, FP8, RB>(vr, cur + C::TILEB, wave, lane);
@@ -419,9 +422,9 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       // rather than left to the compiler's alias tracking of the loads.
       __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
       __syncthreads();
-      const bool more = t + 1 < n_tiles;
       pid = pid_next;
       pid_next = fetch_page_ids(p, ind_lo, npages, t + 2, lane);
+      const int pid_ld = t + 1 < n_tiles ? pid : -1;  // past the last tile: no pages
 
       // ---- S^T = K . Q^T
       f32x16 s[RB][2];
@@ -436,11 +439,11 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
 #pragma unroll
           for (int rb = 0; rb < RB; ++rb) s[rb][mt] = mfma32<BF16>(a, qf[rb][ks_], s[rb][mt]);
         }
-        if (mt == 0 && more) {
+        if (mt == 0) {
           if constexpr (FP8) {
-            load_half<D, BF16, FP8, RB, false>(kr, p, h, pid, npages, last, t + 1, wave, lane);
+            load_half<D, BF16, FP8, RB, false>(kr, p, h, pid_ld, npages, last, t + 1, wave, lane);
           } else {
-            dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid, npages, last, t + 1, nxt, wave,
+            dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid_ld, npages, last, t + 1, nxt, wave,
                                                   lane);
           }
         }
@@ -449,7 +452,6 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       // ---- online softmax in log2 units; lane holds 32 of the tile's 64
       // tokens of its row (token 32 mt + 8 (i/4) + 4 half + i%4 in register i)
       const int tok0 = t * BN;
-      const bool need_mask = tok0 + BN > clean_end;
       float ksc[4], vsc[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -458,7 +460,7 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       }
 #pragma unroll
       for (int rb = 0; rb < RB; ++rb) {
-        if (need_mask) {
+        if constexpr (MASK) {
           const int rel = lim[rb] - tok0 - 4 * half;  // visible iff offset <= rel
 #pragma unroll
           for (int mt = 0; mt < 2; ++mt)
@@ -513,11 +515,11 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       // ---- O^T += V^T . P^T over 4 steps of 16 tokens
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
-        if (st == 1 && more) {
+        if (st == 1) {
           if constexpr (FP8) {
-            load_half<D, BF16, FP8, RB, true>(vr, p, h, pid, npages, last, t + 1, wave, lane);
+            load_half<D, BF16, FP8, RB, true>(vr, p, h, pid_ld, npages, last, t + 1, wave, lane);
           } else {
-            dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid, npages, last, t + 1,
+            dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid_ld, npages, last, t + 1,
                                                  nxt + C::TILEB, wave, lane);
           }
         }
@@ -545,11 +547,30 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
         }
       }
     };
-    for (int t = 0; t < n_tiles; t += 2) {
-      step(t, st0, st1);
-      if (t + 1 >= n_tiles) break;
-      step(t + 1, st1, st0);
-    }
+    // tiles [0, n_clean) lie wholly at or below the first row's diagonal
+    // (and inside the sequence): no mask; the rest are masked.  Tile t uses
+    // stage t & 1 (the prologue loaded tile 0 into stage 0).
+    const int n_clean = min(n_tiles, clean_end / BN);
+    int t = 0;
+    auto run_tiles = [&](auto mask_tag, const int t_end) __attribute__((always_inline)) {
+      if (t < t_end && (t & 1)) {
+        step(mask_tag, t, st1, st0);
+        ++t;
+      }
+      for (; t + 1 < t_end; t += 2) {
+        step(mask_tag, t, st0, st1);
+        step(mask_tag, t + 1, st1, st0);
+      }
+      if (t < t_end) {
+        step(mask_tag, t, st0, st1);
+        ++t;
+      }
+    };
+    run_tiles(std::false_type{}, n_clean);
+    run_tiles(std::true_type{}, n_tiles);
+    // the last tile's loads (of no page) are complete before the workgroup
+    // can end and its LDS be handed on
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
 
     // ---- epilogue: O^T / l, lane's row, 4 consecutive d per register quad
 #pragma unroll
@@ -591,8 +612,6 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
 
 using PrefillFn = void (*)(PrefillParams);
 
-constexpr int kPrefillRB = 1;
-
 template <int D, bool BF16, bool FP8>
 PrefillFn prefill_fn() {
   return prefill_kernel<D, BF16, FP8, kPrefillRB>;
@@ -607,99 +626,11 @@ static PrefillFn pick_prefill(int d, bool bf16, bool fp8) {
   return fp8 ? prefill_fn<128, false, true>() : prefill_fn<128, false, false>();
 }
 
-constexpr int kPrefillRows = kPrefillWaves * 32 * kPrefillRB;
-
-// Paired tiles (a q-tile of at most half a workgroup's rows, run for two KV
-// heads by one workgroup) are planned by default; PAGEDATTN_PREFILL_PAIR=0
-// plans every tile on its own.
-static bool prefill_pairing() {
-  const char* env = std::getenv("PAGEDATTN_PREFILL_PAIR");
-  return !(env && std::atoi(env) == 0);
-}
-
 }  // namespace pa
 
 using namespace pa;
 
 extern "C" {
-
-int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
-                           const int32_t* kv_indptr_host,
-                           const int32_t* kv_last_page_len_host,
-                           int32_t batch_size, int32_t num_qo_heads,
-                           int32_t num_kv_heads, int32_t head_dim,
-                           int32_t page_size, void* workspace,
-                           size_t workspace_bytes, void* stream) {
-  const char* who = "prefill_plan";
-  if (!plan) return set_error(PAGEDATTN_ERR_INVALID, "%s: null plan", who);
-  plan->mode = kPlanNone;
-  if (batch_size < 0)
-    return set_error(PAGEDATTN_ERR_INVALID, "%s: batch_size %d < 0", who,
-                     batch_size);
-  int rc = validate_heads(who, num_qo_heads, num_kv_heads, head_dim, page_size);
-  if (rc) return rc;
-  if (!workspace || ((uintptr_t)workspace & (kWsAlign - 1)))
-    return set_error(PAGEDATTN_ERR_INVALID,
-                     "%s: workspace must be a 256-byte aligned device buffer",
-                     who);
-  if (batch_size > 0 && !qo_indptr_host)
-    return set_error(PAGEDATTN_ERR_INVALID, "%s: null qo_indptr", who);
-  std::vector<int32_t> npages, kv_len;
-  rc = validate_paged_metadata(who, kv_indptr_host, kv_last_page_len_host,
-                               batch_size, page_size, &npages, &kv_len);
-  if (rc) return rc;
-  if (batch_size > 0 && qo_indptr_host[0] < 0)
-    return set_error(PAGEDATTN_ERR_INVALID, "%s: qo_indptr[0] < 0", who);
-  const int g = num_qo_heads / num_kv_heads;
-  const int q_tile = kPrefillRows / g;
-  const bool pair = prefill_pairing() && num_kv_heads % 2 == 0;
-  std::vector<PrefillItem> items;
-  std::vector<int64_t> cost;
-  for (int b = 0; b < batch_size; ++b) {
-    const int qo = qo_indptr_host[b + 1] - qo_indptr_host[b];
-    if (qo < 0)
-      return set_error(PAGEDATTN_ERR_INVALID,
-                       "%s: qo_indptr is not monotone at %d", who, b);
-    for (int lo = 0; lo < qo; lo += q_tile) {
-      const int hi = std::min(qo, lo + q_tile);
-      // slot 1: a paired tile (kernels built without pairing -- e4m3 pools,
-      // D = 64 -- run it like any other)
-      const int flag = pair && (int64_t)(hi - lo) * g <= kPrefillRows / 2 ? 1 : -1;
-      items.push_back(PrefillItem{b, lo, hi, flag});
-      // kv tokens the tile's last row can see (causal)
-      cost.push_back(std::max<int64_t>(
-          0, std::min<int64_t>(kv_len[b], (int64_t)kv_len[b] - qo + hi)));
-    }
-  }
-  // most expensive tiles first
-  std::vector<int> order(items.size());
-  for (size_t i = 0; i < order.size(); ++i) order[i] = (int)i;
-  std::stable_sort(order.begin(), order.end(),
-                   [&](int a, int c) { return cost[a] > cost[c]; });
-  const size_t host_bytes = sizeof(PrefillItem) * items.size();
-  plan->host.assign((host_bytes + 3) / 4, 0);
-  auto* dst = reinterpret_cast<PrefillItem*>(plan->host.data());
-  for (size_t i = 0; i < order.size(); ++i) dst[i] = items[order[i]];
-  plan->workspace = workspace;
-  plan->workspace_bytes = workspace_bytes;
-  rc = upload_plan(plan, who, host_bytes, ws_align(kWsHeader + host_bytes),
-                   stream);
-  if (rc) return rc;
-  plan->batch_size = batch_size;
-  plan->hq = num_qo_heads;
-  plan->hkv = num_kv_heads;
-  plan->d = head_dim;
-  plan->page_size = page_size;
-  plan->n_items = (int)items.size();
-  plan->n_merge = 0;
-  plan->n_slots = 0;
-  plan->q_tile = q_tile;
-  plan->total_qo =
-      batch_size > 0 ? (int64_t)qo_indptr_host[batch_size] - qo_indptr_host[0] : 0;
-  plan->items_dev = static_cast<char*>(workspace) + kWsHeader;
-  plan->mode = kPlanPrefill;
-  return PAGEDATTN_OK;
-}
 
 int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
                           int64_t q_stride_n, int64_t q_stride_h,
