@@ -562,6 +562,9 @@ DECODE_KERNEL = {
     "c4b": "decode step: decode_kernel<128, bf16, append>, planner's balanced split "
            "+ decode_merge_kernel",
     "c5d": "decode step: decode_kernel<128, e4m3 pool, append> + decode_merge_kernel",
+    "c5d.shared": "decode step: decode_shared_kernel<128, e4m3 pool, append> (each "
+                  "sequence's new K/V written, then attention; whole (sequence, KV head) "
+                  "items shared by the four waves of one workgroup per CU, one launch)",
 }
 PREFILL_KERNEL = {
     "c3": "prefill_kernel<128, bf16> (causal, ragged, paged; bf16 MFMA)",
@@ -644,7 +647,8 @@ def main() -> int:
             rng = __import__("numpy").random.default_rng(5)
             rows = sorted(rng.choice(dec5.meta.batch_size, 8, replace=False).tolist())
             d5 = bench_decode(dec5, sub, dev, dtype, "llama3_70b_mixed_fp8.decode",
-                              rows if cpu else None, DECODE_KERNEL["c5d"])
+                              rows if cpu else None,
+                              {"split": DECODE_KERNEL["c5d"], "shared": DECODE_KERNEL["c5d.shared"]})
             log(f"llama3_70b_mixed_fp8 decode: {d5['step_GBps']:.0f} GB/s "
                 f"({100 * d5['frac']:.1f}%)")
             c5["decode"] = d5

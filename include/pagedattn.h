@@ -115,12 +115,14 @@ int pagedattn_apply_rope_pos_ids_inplace(
  * otherwise); a block whose scale is not positive and finite gets zero
  * codes.  kv_last_page_len is accepted for interface parity and, as in the
  * reference kernel, not used for addressing (may be NULL).
- * *error_flag (int32, device; may be NULL) is incremented once per token
- * whose batch index, page slot or page id fall outside the metadata (the
- * token is skipped) and, for E4M3, once per 8-element piece of a written
+ * error_flag (device int32, may be NULL): error_flag[0] is incremented once
+ * per token whose batch index, page slot or page id fall outside the
+ * metadata (the token is skipped).  For an E4M3 cache error_flag holds two
+ * int32: error_flag[1] is incremented once per 8-element piece of a written
  * row (elements [8i, 8i+8) of one K or V head row) in which some
- * |x / scale| exceeded 448 or whose scale was not positive and finite.
- * Zero after a call means every token landed unclamped. */
+ * |x / scale| exceeded 448 or whose scale was not positive and finite, so a
+ * skipped token and a clamped value stay apart.  Both zero after a call
+ * means every token landed unclamped. */
 int pagedattn_append_paged_kv_cache(
     const void* append_key, const void* append_value, int64_t k_stride_n,
     int64_t k_stride_h, int64_t v_stride_n, int64_t v_stride_h,
@@ -216,8 +218,9 @@ int pagedattn_fork_pages(void* kv_pool, int32_t pool_dtype, int32_t num_layers,
  *     every new token (kv_lens[b] - n .. kv_lens[b] - 1).
  * One launch for batches up to 1024 sequences, two above, all with fixed
  * shapes (graph-capturable).  A row needing more than max_pages pages is
- * cut to them and outputs beyond a capacity are dropped; both are counted in
- * *error_flag. */
+ * cut to them and outputs beyond a capacity are dropped; *error_flag is
+ * incremented once per sequence whose row was cut and once per sequence
+ * some of whose outputs were dropped, by both launch shapes. */
 int pagedattn_build_paged_metadata(const int32_t* block_tables, int64_t table_stride,
                                    int32_t max_pages, const int32_t* kv_lens,
                                    const int32_t* new_lens, int32_t batch_size,
@@ -236,9 +239,12 @@ int pagedattn_build_paged_metadata(const int32_t* block_tables, int64_t table_st
  * planner choose from the device's CU count; -1 disables splitting.
  * The work list and split partials are placed in `workspace` (device,
  * 256-byte aligned, workspace_bytes long) from byte 256 on, with one
- * hipMemcpyAsync on `stream`.  Bytes [0, 256) are the caller's, except the
- * int32 at byte 0: the error counter that the fused-append decode runs
- * increment (never cleared by the library). */
+ * hipMemcpyAsync on `stream`.  Bytes [0, 256) are the caller's, except
+ * three int32 counters that runs increment and the library never clears:
+ * byte 0, tokens the fused-append decode runs skipped; byte 4, e4m3 pieces
+ * they clamped; byte 8, merge-slot waits of a shared-item decode run that
+ * gave up (never in a consistent run: the item's output is then left
+ * unwritten rather than merged wrongly). */
 pagedattn_plan* pagedattn_plan_create(void);
 void pagedattn_plan_destroy(pagedattn_plan* plan);
 
@@ -275,12 +281,14 @@ int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
  * CU-sized workgroup whose waves share each item's pages; one launch),
  * PAGEDATTN_DECODE_DEVICE (partition made on the device at run time), or 0
  * for a plan that is not a decode plan.  pagedattn_decode_plan with
- * split_pages = 0 takes a shared plan at head_dim 64 when its busiest CU
- * carries at most PAGEDATTN_DECODE_SHARED_SLACK_KB (environment, default 96)
- * KiB more K/V than the mean; PAGEDATTN_DECODE_SHARED=0 / =1 turns that off
- * / takes one whenever it fits.  A shared plan's waves take page pairs in
- * arrival order, so repeated runs can differ in the last bits of the output;
- * PAGEDATTN_DECODE_DETERMINISTIC=1 (read at plan time) fixes the order. */
+ * split_pages = 0 takes a shared plan when its busiest CU carries at most
+ * PAGEDATTN_DECODE_SHARED_SLACK_KB (environment, default 96) KiB plus
+ * PAGEDATTN_DECODE_SHARED_SLACK_PCT (default 4) percent of the mean more K/V
+ * than the mean; PAGEDATTN_DECODE_SHARED=0 / =1 turns that off / takes one
+ * whenever it fits.  A shared plan's waves take fixed page pairs, so repeated
+ * runs give identical bits; PAGEDATTN_DECODE_DETERMINISTIC=0 (read at plan
+ * time) lets them claim pairs in arrival order instead, which balances the
+ * waves of a workgroup but lets the last bits of the output vary. */
 #define PAGEDATTN_DECODE_SPLIT 1
 #define PAGEDATTN_DECODE_SHARED 2
 #define PAGEDATTN_DECODE_DEVICE 3
@@ -312,9 +320,9 @@ int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
  * step must be arange(B) (src/engine/runtime/step_executor.py:220-222);
  * other token orders go through pagedattn_append_paged_kv_cache and
  * pagedattn_decode_run.  A sequence (with pages) whose new token falls
- * outside its pages or on an invalid page id is not appended, and e4m3
- * pieces clamped as in pagedattn_append_paged_kv_cache are counted, in the
- * int32 at byte 0 of the plan's workspace.
+ * outside its pages or on an invalid page id is not appended and counted in
+ * the int32 at byte 0 of the plan's workspace; e4m3 pieces clamped as in
+ * pagedattn_append_paged_kv_cache are counted in the int32 at byte 4.
  * Same plan, pool and output contract as pagedattn_decode_run. */
 int pagedattn_decode_run_append(
     const pagedattn_plan* plan, const void* q, int64_t q_stride_n,

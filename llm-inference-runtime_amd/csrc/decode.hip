@@ -78,8 +78,11 @@ struct DecodeParams {
   const int32_t* new_pos;
   double rope_inv_scale, rope_log2_theta;
   // fused append: tokens skipped (position outside the sequence's pages or
-  // an invalid page id) and clamped e4m3 chunks are counted here (may be null)
+  // an invalid page id) are counted at append_err[0], clamped e4m3 pieces at
+  // append_err[1] (may be null)
   int32_t* append_err;
+  // shared-item plans: slot waits that gave up (never in a consistent run)
+  int32_t* fault_count;
 };
 
 template <int N>
@@ -468,7 +471,7 @@ __device__ __forceinline__ void put_chunk(const DecodeParams& p, int h, int page
     bool clamped = false;
     const u32x2 q = quant8_e4m3<BF16>(x, scale, &clamped);
     *reinterpret_cast<u32x2*>(dst) = q;
-    count_lanes(p.append_err, clamped);
+    count_lanes(p.append_err ? p.append_err + 1 : nullptr, clamped);
   } else {
     *reinterpret_cast<u32x4*>(dst) = x;
   }
@@ -754,19 +757,25 @@ __global__ void __launch_bounds__(256, 1) decode_kernel(DecodeParams p) {
 // writes the output.  No sequence is
 // cut across workgroups, so there are no split partials and no merge launch.
 
-constexpr int kSharedSlots = 2;     // items whose states can wait in LDS at once
+// Items whose states can wait in LDS at once: with the fixed chunk
+// assignment a wave that runs ahead by more items than this waits for a slot
+// to be merged (three at D = 128 keep the workgroup's LDS under 160 KiB).
+template <int D>
+constexpr int shared_slots() { return D == 64 ? 4 : 3; }
 // Bound of the wait for a slot to be released (each round sleeps ~64 clocks);
 // the wait always ends long before, since a slot only waits for items of
-// lower index, whose waves never wait for it.
+// lower index, whose waves never wait for it.  A wait that gives up counts
+// in DecodeParams::fault_count and writes nothing.
 constexpr int kSharedSpinLimit = 1 << 24;
 
 template <int D>
 struct SharedLds {
   int total;      // chunks of the workgroup's items
   int next;       // chunk counter (claims in arrival order)
-  int tag[kSharedSlots];   // item index the slot is open for
-  int cnt[kSharedSlots];   // chunks accounted for by the states left in the slot
-  int mask[kSharedSlots];  // waves whose states are in the slot
+  static constexpr int S = shared_slots<D>();
+  int tag[S];   // item index the slot is open for
+  int cnt[S];   // chunks accounted for by the states left in the slot
+  int mask[S];  // waves whose states are in the slot
   int b[kSharedMaxItems], h[kSharedMaxItems], chunk_lo[kSharedMaxItems],
       n_chunks[kSharedMaxItems], ind_lo[kSharedMaxItems], npages[kSharedMaxItems],
       last[kSharedMaxItems], new_pos[kSharedMaxItems];
@@ -774,7 +783,7 @@ struct SharedLds {
   struct State {
     f32x4 o[D / 16][kWave];
     float m[kWave], l[kWave];
-  } st[kSharedSlots][4];
+  } st[S][4];
 };
 
 // A claimed chunk: item index in the workgroup's table (-1: none left) and
@@ -836,7 +845,7 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
       if (t == n_it - 1) L.total = it.chunk_lo + max(it.n_chunks, 0);
     }
     if (t == 0) L.next = 0;
-    if (t < kSharedSlots) {
+    if (t < SharedLds<D>::S) {
       L.tag[t] = t;
       L.cnt[t] = 0;
       L.mask[t] = 0;
@@ -872,11 +881,10 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
       qtmp[k][ks] = *reinterpret_cast<const u32x4*>(qrow + 32 * ks + 8 * G);
   }
 
-  // chunks are claimed in arrival order through an LDS counter, so a wave
-  // that streams more slowly takes fewer (TinyLlama B=256 step 54.4-55.0 us
-  // against 56.0-56.8 us with a fixed assignment, same runs); with
-  // p.deterministic wave w takes chunks w, w + 4, w + 8, ..., so the states
-  // merged per item (and the output bits) do not depend on timing
+  // with p.deterministic (the default) wave w takes chunks w, w + 4, w + 8,
+  // ..., so the states merged per item (and the output bits) do not depend on
+  // timing; otherwise chunks are claimed in arrival order through an LDS
+  // counter, so a wave that streams more slowly takes fewer
   int next_chunk = wave;
   auto claim = [&]() -> ChunkRef {
     int c;
@@ -939,27 +947,44 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
     }
   };
 
-  // ---- appends: the wave of item i writes its new K/V rows, waits for the
-  // stores, and the barrier orders them before every wave's first K/V load
-  // (any wave may load the page); without appends the first chunk's loads
-  // are issued before the barrier
+  // ---- appends: item i's new K/V rows are written to the pool before any
+  // wave loads that page.  With the fixed chunk assignment the wave that
+  // will load the chunk holding the new row writes it itself: its own store
+  // precedes its load of those addresses in program order, so no wait and
+  // no barrier is needed, and the first chunk's loads are issued before the
+  // Q barrier.  With arrival-order claims any wave may load the page: the
+  // item's wave writes the rows, waits for the stores, and the barrier
+  // orders them before every wave's first K/V load.
+  const bool det = p.deterministic != 0;
+  auto append_item = [&](int i) {
+    const int b = field(t_b, i), h = field(t_h, i), np = field(t_np, i), pos = field(t_pos, i);
+    const int pg = pos >= 0 ? pos / kPage : -1;
+    if (b < 0 || pg < 0 || pg >= np) return;
+    const int page = page_id(p, field(t_ind, i), pg, np);
+    if (page >= 0)
+      fused_append<D, BF16, FP8, ROPE>(p, b, h, page, pos & (kPage - 1), lane, pos);
+    else
+      count_lanes(p.append_err, h == 0 && lane == 0);
+  };
   if constexpr (APPEND) {
+    if (det) {
+      // chunk chunk_lo + pg / (2 NP) holds page pg of item i; wave (chunk
+      // mod 4) claims it
+      for (int i = 0; i < n_it; ++i) {
+        const int pos = field(t_pos, i);
+        const int pg = pos >= 0 ? pos / kPage : 0;
+        if (((field(t_lo, i) + pg / (2 * NP)) & 3) == wave) append_item(i);
+      }
+    } else {
 #pragma unroll
-    for (int k = 0; k < QPW; ++k) {
-      const int i = wave + 4 * k;
-      if (i >= n_it) continue;
-      const int b = field(t_b, i), h = field(t_h, i), np = field(t_np, i), pos = field(t_pos, i);
-      const int pg = pos >= 0 ? pos / kPage : -1;
-      if (b < 0 || pg < 0 || pg >= np) continue;
-      const int page = page_id(p, field(t_ind, i), pg, np);
-      if (page >= 0)
-        fused_append<D, BF16, FP8, ROPE>(p, b, h, page, pos & (kPage - 1), lane, pos);
-      else
-        count_lanes(p.append_err, h == 0 && lane == 0);
+      for (int k = 0; k < QPW; ++k) {
+        const int i = wave + 4 * k;
+        if (i < n_it) append_item(i);
+      }
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the appended rows are in L2
+      store_q();
+      __syncthreads();
     }
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the appended rows are in L2
-    store_q();
-    __syncthreads();
   }
 
   Stage<D, BF16, FP8> sa[NP], sb[NP];
@@ -969,7 +994,7 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
   ChunkRef rb = claim();
   fetch(idb, rb);
   load(sa, ida, ra);
-  if constexpr (!APPEND) {
+  if (!APPEND || det) {
     store_q();
     __syncthreads();
   }
@@ -981,12 +1006,25 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
   // leaves the state of item i in its slot; the wave that completes the
   // item's chunk count merges every state there and writes the output
   auto flush = [&](int i, int k) {
-    const int s = i % kSharedSlots;
-    for (int spin = 0;; ++spin) {
-      const int tg = uniform(__hip_atomic_load(&L.tag[s], __ATOMIC_RELAXED,
+    const int s = i % SharedLds<D>::S;
+    // the acquire pairs with the release that reopened the slot, so the
+    // previous item's resets and reads of the slot come before this write
+    bool open = false;
+    for (int spin = 0; spin < kSharedSpinLimit; ++spin) {
+      const int tg = uniform(__hip_atomic_load(&L.tag[s], __ATOMIC_ACQUIRE,
                                                __HIP_MEMORY_SCOPE_WORKGROUP));
-      if (tg == i || spin >= kSharedSpinLimit) break;
+      if (tg == i) {
+        open = true;
+        break;
+      }
       __builtin_amdgcn_s_sleep(1);
+    }
+    if (!open) {
+      // never reached in a consistent run (a slot only waits for items of
+      // lower index, whose waves never wait for it); leave the slot alone
+      // and count the item as not written rather than corrupt another's state
+      count_lanes(p.fault_count, lane == 0);
+      return;
     }
     typename SharedLds<D>::State& mine = L.st[s][wave];
 #pragma unroll
@@ -1029,7 +1067,7 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
     if (lane == 0) {
       __hip_atomic_store(&L.cnt[s], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       __hip_atomic_store(&L.mask[s], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      __hip_atomic_store(&L.tag[s], i + kSharedSlots, __ATOMIC_RELEASE,
+      __hip_atomic_store(&L.tag[s], i + SharedLds<D>::S, __ATOMIC_RELEASE,
                          __HIP_MEMORY_SCOPE_WORKGROUP);
     }
   };
@@ -1224,7 +1262,8 @@ DecodeFn decode_shared_fn_d(bool bf16, bool fp8, bool append, bool rope) {
 }
 
 static DecodeFn pick_decode_shared(int d, bool bf16, bool fp8, bool append, bool rope) {
-  return d == 64 ? decode_shared_fn_d<64>(bf16, fp8, append, rope) : nullptr;
+  return d == 64 ? decode_shared_fn_d<64>(bf16, fp8, append, rope)
+                 : decode_shared_fn_d<128>(bf16, fp8, append, rope);
 }
 
 static DecodeFn pick_decode(int d, bool bf16, bool fp8, bool append, bool rope, bool implicit) {
@@ -1251,7 +1290,8 @@ struct AppendRows {
   const int32_t* new_pos;
   double rope_inv_scale, rope_log2_theta;
   // fused append: tokens skipped (position outside the sequence's pages or
-  // an invalid page id) and clamped e4m3 chunks are counted here (may be null)
+  // an invalid page id) are counted at append_err[0], clamped e4m3 pieces at
+  // append_err[1] (may be null)
   int32_t* append_err;
 };
 
@@ -1330,6 +1370,8 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   p.rope_inv_scale = app ? app->rope_inv_scale : 1.0;
   p.rope_log2_theta = app ? app->rope_log2_theta : 0.0;
   p.append_err = app ? app->append_err : nullptr;
+  // int32 2 of the workspace header (plan workspaces; noalloc runs have none)
+  p.fault_count = plan->workspace ? static_cast<int32_t*>(plan->workspace) + 2 : nullptr;
 
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = q_dtype == PAGEDATTN_BF16;
@@ -1408,7 +1450,8 @@ int pagedattn_decode_run_append(
                      "%s: append rows must be 16-byte aligned with strides that "
                      "are multiples of 8 elements",
                      who);
-  // skips and clamps are counted in the int32 at byte 0 of the workspace
+  // skipped tokens are counted in the int32 at byte 0 of the workspace,
+  // clamped e4m3 pieces in the one at byte 4
   AppendRows app{append_key, append_value, k_stride_n, k_stride_h,
                  v_stride_n, v_stride_h, q_dtype, false, nullptr, 1.0, 0.0,
                  plan ? static_cast<int32_t*>(plan->workspace) : nullptr};

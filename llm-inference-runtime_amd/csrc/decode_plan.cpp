@@ -54,9 +54,12 @@ static int decode_head_group(int hkv) {
 // Shared-item plans (decode_shared_kernel): PAGEDATTN_DECODE_SHARED=0 turns
 // them off, =1 takes one whenever the items fit a workgroup's table; by
 // default one is taken when its busiest CU holds at most
-// PAGEDATTN_DECODE_SHARED_SLACK_KB KiB more K/V than the mean (default 96:
-// what one CU streams in about the 4-5 us that the split's merge launch
-// costs).
+// PAGEDATTN_DECODE_SHARED_SLACK_KB KiB (default 96: what one CU streams in
+// the 4-5 us that the split's merge launch costs) plus
+// PAGEDATTN_DECODE_SHARED_SLACK_PCT percent of the mean (default 4: the
+// split's partials and per-item restarts) more K/V than the mean.  Measured
+// on the 70B-shaped e4m3 batch (D = 128, busiest CU 3.1 % over the mean):
+// 214 us shared against 225 us split.
 static int decode_shared_mode() {
   if (const char* env = std::getenv("PAGEDATTN_DECODE_SHARED")) {
     const int v = std::atoi(env);
@@ -64,12 +67,14 @@ static int decode_shared_mode() {
   }
   return -1;
 }
-// Shared plans claim chunks in arrival order (fastest);
-// PAGEDATTN_DECODE_DETERMINISTIC=1 gives them a fixed chunk assignment,
-// whose output bits do not depend on timing.
+// Shared plans give wave w of a workgroup the chunks w, w + 4, w + 8, ...,
+// so the output bits do not depend on timing (as FlashInfer's decode);
+// PAGEDATTN_DECODE_DETERMINISTIC=0 lets the waves claim chunks in arrival
+// order instead, which balances the waves of a workgroup but makes the last
+// bits of the output vary from run to run.
 static bool decode_deterministic() {
   const char* env = std::getenv("PAGEDATTN_DECODE_DETERMINISTIC");
-  return env && std::atoi(env) == 1;
+  return !(env && std::atoi(env) == 0);
 }
 
 static int64_t decode_shared_slack_bytes() {
@@ -78,6 +83,13 @@ static int64_t decode_shared_slack_bytes() {
     if (v >= 0) return (int64_t)v << 10;
   }
   return (int64_t)96 << 10;
+}
+static int decode_shared_slack_pct() {
+  if (const char* env = std::getenv("PAGEDATTN_DECODE_SHARED_SLACK_PCT")) {
+    const int v = std::atoi(env);
+    if (v >= 0 && v <= 100) return v;
+  }
+  return 4;
 }
 
 // Shared-item partition: whole (sequence, KV head) items, longest first onto
@@ -89,9 +101,7 @@ static bool plan_shared(const std::vector<int32_t>& npages, int hkv, int d, int 
                         std::vector<SharedItem>* items, std::vector<int32_t>* wg_ptr) {
   const int batch = (int)npages.size();
   const int64_t n_all = (int64_t)batch * hkv;
-  // built for D = 64: at D = 128 two register stages, the merge and the
-  // output conversion do not fit the register file together
-  if (n_all == 0 || d != 64) return false;
+  if (n_all == 0) return false;
   const int chunk_pages = 2 * kSharedStagePairs;
   std::vector<int32_t> order((size_t)n_all);
   for (int64_t i = 0; i < n_all; ++i) order[(size_t)i] = (int32_t)i;
@@ -122,7 +132,11 @@ static bool plan_shared(const std::vector<int32_t>& npages, int hkv, int d, int 
   }
   // K and V of one page of one KV head, counted at 16 bits per element
   const int64_t page_bytes = (int64_t)kPage * d * 2 * 2;
-  if (!forced && (mx * n_wg - sum) * page_bytes > decode_shared_slack_bytes() * n_wg) return false;
+  // busiest - mean > slack + pct% of the mean, scaled by n_wg
+  if (!forced && (mx * n_wg - sum) * page_bytes * 100 >
+                     decode_shared_slack_bytes() * n_wg * 100 +
+                         sum * page_bytes * decode_shared_slack_pct())
+    return false;
   items->clear();
   wg_ptr->assign(1, 0);
   for (int w = 0; w < n_wg; ++w) {

@@ -49,6 +49,15 @@ __device__ __forceinline__ int seq_new_tokens(const MetaArgs& a, int b, int L) {
   return min(max(a.new_lens[b], 0), max(L, 0));
 }
 
+// Whether some of sequence b's outputs fall past a capacity (or behind an
+// offset that overflowed int32): decided from its offsets, so the sequence
+// is counted once whatever the grid.
+__device__ __forceinline__ bool seq_dropped(const MetaArgs& a, int off, int np, int qo, int nt) {
+  const bool pages = np > 0 && (off < 0 || (int64_t)off + np > a.indices_cap);
+  const bool toks = a.new_lens && nt > 0 && (qo < 0 || (int64_t)qo + nt > a.tokens_cap);
+  return pages || toks;
+}
+
 // Exclusive prefix sum over the 1024 threads of the workgroup; *total gets
 // the sum.  `red` holds 16 wave totals.
 __device__ __forceinline__ int block_excl_scan(int v, int* total, int* red) {
@@ -79,14 +88,14 @@ __device__ __forceinline__ int block_excl_scan(int v, int* total, int* red) {
 __global__ void __launch_bounds__(kMetaThreads) meta_scan_kernel(MetaArgs a) {
   __shared__ int red[2][kMetaThreads / kWave];
   int run_pages = 0, run_tokens = 0;
-  bool clipped = false;
+  int clipped = 0;
   for (int base = 0; base < a.batch; base += kMetaThreads) {
     const int b = base + (int)threadIdx.x;
     const int L = b < a.batch ? a.kv_lens[b] : 0;
     const int full = L > 0 ? (L + kPage - 1) / kPage : 0;
     const int np = b < a.batch ? seq_pages(a, L) : 0;
     const int nt = b < a.batch ? seq_new_tokens(a, b, L) : 0;
-    clipped |= full > np;
+    clipped += full > np ? 1 : 0;
     int tot_p, tot_t;
     const int ep = block_excl_scan(np, &tot_p, red[0]);
     const int et = block_excl_scan(nt, &tot_t, red[1]);
@@ -102,7 +111,7 @@ __global__ void __launch_bounds__(kMetaThreads) meta_scan_kernel(MetaArgs a) {
     run_pages += tot_p;
     run_tokens += tot_t;
   }
-  if (__syncthreads_or(clipped) && threadIdx.x == 0 && a.err) atomicAdd(a.err, 1);
+  if (clipped > 0 && a.err) atomicAdd(a.err, clipped);
   if (threadIdx.x == 0) {
     a.kv_indptr[a.batch] = run_pages;
     if (a.qo_indptr) a.qo_indptr[a.batch] = run_tokens;
@@ -111,8 +120,8 @@ __global__ void __launch_bounds__(kMetaThreads) meta_scan_kernel(MetaArgs a) {
 
 // Grid (x, b): the page ids of sequence b copied out of its table row, and
 // (prefill) its new tokens' sequence / position rows.  Entries past the
-// output capacities (or behind offsets that overflowed int32) are dropped and
-// counted once per sequence.
+// output capacities (or behind offsets that overflowed int32) are dropped;
+// the sequence is counted once.
 __global__ void __launch_bounds__(256) meta_fill_kernel(MetaArgs a) {
   const int b = blockIdx.y;
   const int L = a.kv_lens[b];
@@ -121,32 +130,30 @@ __global__ void __launch_bounds__(256) meta_fill_kernel(MetaArgs a) {
   const int step = gridDim.x * blockDim.x;
   const int first = blockIdx.x * blockDim.x + threadIdx.x;
   const int32_t* row = a.tables + (int64_t)b * a.stride;
-  bool over = false;
-  for (int i = first; i < np; i += step) {
+  for (int i = first; i < np; i += step)
     if (off >= 0 && (int64_t)off + i < a.indices_cap) a.kv_indices[off + i] = row[i];
-    else over = true;
-  }
+  const int nt = seq_new_tokens(a, b, L);
+  const int qo = a.new_lens ? a.qo_indptr[b] : 0;
   if (a.new_lens) {
-    const int nt = seq_new_tokens(a, b, L);
-    const int qo = a.qo_indptr[b];
     for (int j = first; j < nt; j += step) {
       const int64_t t = (int64_t)qo + j;
       if (qo >= 0 && t < a.tokens_cap) {
         a.bi[t] = b;
         a.pos[t] = L - nt + j;
-      } else {
-        over = true;
       }
     }
   }
-  if (__syncthreads_or(over) && threadIdx.x == 0 && a.err) atomicAdd(a.err, 1);
+  if (blockIdx.x == 0 && threadIdx.x == 0 && a.err && seq_dropped(a, off, np, qo, nt))
+    atomicAdd(a.err, 1);
 }
 
 // Batches up to kMetaFuseMax sequences: one launch, grid (x, b).  Every
 // workgroup of sequence b sums the page and token counts of the sequences
 // before it itself (at most kMetaFuseMax loads per workgroup), so no
 // workgroup waits for another; then it writes what the scan and the fill
-// kernels write for b.  A clipped row is counted once per sequence.
+// kernels write for b.  A clipped row, and a sequence some of whose outputs
+// were dropped, are each counted once per sequence (as the two-launch path
+// counts them).
 constexpr int kMetaFuseMax = 1024;
 constexpr int kMetaFuseThreads = 256;
 
@@ -198,23 +205,19 @@ __global__ void __launch_bounds__(kMetaFuseThreads) meta_fused_kernel(MetaArgs a
   const int step = gridDim.x * blockDim.x;
   const int first = blockIdx.x * blockDim.x + threadIdx.x;
   const int32_t* row = a.tables + (int64_t)b * a.stride;
-  bool over = false;
-  for (int i = first; i < np; i += step) {
+  for (int i = first; i < np; i += step)
     if (off >= 0 && (int64_t)off + i < a.indices_cap) a.kv_indices[off + i] = row[i];
-    else over = true;
-  }
   if (a.new_lens) {
     for (int j = first; j < nt; j += step) {
       const int64_t t = (int64_t)qo + j;
       if (qo >= 0 && t < a.tokens_cap) {
         a.bi[t] = b;
         a.pos[t] = L - nt + j;
-      } else {
-        over = true;
       }
     }
   }
-  if (__syncthreads_or(over) && threadIdx.x == 0 && a.err) atomicAdd(a.err, 1);
+  if (blockIdx.x == 0 && threadIdx.x == 0 && a.err && seq_dropped(a, off, np, qo, nt))
+    atomicAdd(a.err, 1);
 }
 
 }  // namespace pa

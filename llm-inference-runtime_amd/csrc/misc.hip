@@ -65,7 +65,7 @@ __global__ void __launch_bounds__(256)
 // ----------------------------------------------------------------------------
 // Writes one 8-element chunk of a K (kind 0) or V (kind 1) row of head h to
 // slot `slot` of `page`.  e4m3 pools: quantised with the page's fixed scale
-// (quant8_e4m3); a clamped chunk is counted in *a.err.
+// (quant8_e4m3); a clamped chunk is counted in a.err[1].
 template <bool IS_BF16, bool TO_FP8>
 __device__ __forceinline__ void store_chunk(const AppendArgs& a, int64_t page, int slot,
                                             int kind, int h, int d0, u32x4 x) {
@@ -78,15 +78,15 @@ __device__ __forceinline__ void store_chunk(const AppendArgs& a, int64_t page, i
     bool clamped = false;
     const u32x2 o = quant8_e4m3<IS_BF16>(x, scale, &clamped);
     *reinterpret_cast<u32x2*>(static_cast<uint8_t*>(a.cache) + dst_elem) = o;
-    count_lanes(a.err, clamped);
+    count_lanes(a.err ? a.err + 1 : nullptr, clamped);
   }
 }
 
 // append_paged_kv_cache (src/models/llama.py:188-210), HND pool.  One thread
 // moves one 16-byte chunk (8 elements) of one head of K or V, so a wave
 // writes whole 128/256-byte page rows.  Metadata outside its ranges skips the
-// token and bumps *err instead of faulting (once per token); e4m3 chunks
-// whose values were clamped bump it once per chunk.
+// token and bumps err[0] instead of faulting (once per token); e4m3 chunks
+// whose values were clamped bump err[1] once per chunk.
 template <bool FP8_IS_BF16_SRC, bool TO_FP8>
 __global__ void __launch_bounds__(256) append_kernel(AppendArgs a) {
   const int chunks = a.d >> 3;  // 8 elements per chunk

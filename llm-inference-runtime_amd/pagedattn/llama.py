@@ -94,15 +94,26 @@ def init_flashinfer_state(*, kv_pool: torch.Tensor, page_size: int, device,
 
 
 def append_error_count() -> int:
-    """The page appends' error counter since init (reads the device counter:
-    synchronises): tokens skipped because their metadata pointed outside the
-    page table, plus, for e4m3 pools with fixed scales, 8-element pieces of
-    written rows that were clamped at +-448 (or met a bad scale).  The fused
-    decode launches count into the same int32 (byte 0 of the workspace)."""
+    """Tokens the page appends skipped since init because their metadata
+    pointed outside the page table (reads the device counter: synchronises).
+    Every append path, the fused decode launches included, counts into the
+    int32 at byte 0 of the workspace."""
     ws = FlashInferState.workspace_buffer
     if ws is None:
         return 0
     return int(ws[:4].view(torch.int32)[0].item())
+
+
+def append_clamp_count() -> int:
+    """8-element pieces of rows written to an e4m3 pool with fixed scales
+    that were clamped at +-448 (or met a bad scale) since init (synchronises;
+    the int32 at byte 4 of the workspace).  Kept apart from
+    append_error_count(): clamps are routine with scales taken from earlier
+    rows, skipped tokens are not."""
+    ws = FlashInferState.workspace_buffer
+    if ws is None:
+        return 0
+    return int(ws[4:8].view(torch.int32)[0].item())
 
 
 def build_batch_indices_positions(append_indptr: torch.Tensor, seq_lens: torch.Tensor) -> None:
@@ -207,7 +218,7 @@ def patched_llama_attention_forward(self, hidden_states: torch.Tensor,
             layer_pool, cast(torch.Tensor, FlashInferState.kv_indices),
             cast(torch.Tensor, FlashInferState.kv_indptr),
             cast(torch.Tensor, FlashInferState.kv_last_page_len), layer_scales,
-            kv_layout="HND", error_flag=ws[:4].view(torch.int32))
+            kv_layout="HND", error_flag=ws[:8].view(torch.int32))
     elif FUSE and decode and _decode_rows_match(q_rows):
         # RoPE + append + attention of the decode step in one launch
         dw = cast(ops.BatchDecodeWithPagedKVCacheWrapper, FlashInferState.decode_wrapper)
@@ -223,7 +234,7 @@ def patched_llama_attention_forward(self, hidden_states: torch.Tensor,
             cast(torch.Tensor, FlashInferState.kv_indptr),
             cast(torch.Tensor, FlashInferState.kv_last_page_len), kv_layout="HND",
             rope_scale=self.rope_scale, rope_theta=self.rope_theta, kv_scales=layer_scales,
-            error_flag=ws[:4].view(torch.int32))
+            error_flag=ws[:8].view(torch.int32))
     else:
         ops.apply_rope_pos_ids_inplace(q_rows, k_rows, positions, rope_theta=self.rope_theta,
                                        rope_scale=self.rope_scale, interleave=False)
@@ -232,7 +243,7 @@ def patched_llama_attention_forward(self, hidden_states: torch.Tensor,
             layer_pool, cast(torch.Tensor, FlashInferState.kv_indices),
             cast(torch.Tensor, FlashInferState.kv_indptr),
             cast(torch.Tensor, FlashInferState.kv_last_page_len), kv_layout="HND",
-            kv_scales=layer_scales, error_flag=ws[:4].view(torch.int32))
+            kv_scales=layer_scales, error_flag=ws[:8].view(torch.int32))
 
     if not decode:
         pw = cast(ops.BatchPrefillWithPagedKVCacheWrapper, FlashInferState.prefill_wrapper)

@@ -155,6 +155,15 @@ def apply_rope_pos_ids_inplace(q: torch.Tensor, k: torch.Tensor, pos_ids: torch.
          _stream(q.device))
 
 
+def _check_error_flag(error_flag: torch.Tensor | None, n: int) -> None:
+    if error_flag is None:
+        return
+    if (error_flag.dtype != torch.int32 or error_flag.numel() < n
+            or not error_flag.is_contiguous() or error_flag.device.type != "cuda"):
+        raise ValueError(f"error_flag must be a contiguous int32 device tensor of at least {n} "
+                         "entries")
+
+
 def append_paged_kv_cache(append_key: torch.Tensor, append_value: torch.Tensor,
                           batch_indices: torch.Tensor, positions: torch.Tensor,
                           paged_kv_cache: torch.Tensor, kv_indices: torch.Tensor,
@@ -166,10 +175,12 @@ def append_paged_kv_cache(append_key: torch.Tensor, append_value: torch.Tensor,
     Bit-exact for a pool of the source dtype; an e4m3 pool stores
     round(clamp(x / scale, +-448)) with kv_scales [num_pages, 2, Hkv] (zero
     codes where a scale is not positive and finite).
-    `error_flag` (int32 device scalar, optional) is incremented once per
-    token whose metadata pointed outside the page table (the token is
-    skipped) and, for e4m3, once per 8-element piece of a written row that
-    was clamped or had a bad scale; zero means every token landed intact."""
+    `error_flag` (int32 device tensor, optional): error_flag[0] is
+    incremented once per token whose metadata pointed outside the page table
+    (the token is skipped); for an e4m3 pool it holds two int32 and
+    error_flag[1] is incremented once per 8-element piece of a written row
+    that was clamped or had a bad scale.  Zeros mean every token landed
+    intact."""
     num_pages, hkv, d = _check_pool(paged_kv_cache, None, None, kv_layout)
     _check_rows(append_key, "append_key", hkv, d)
     _check_rows(append_value, "append_value", hkv, d)
@@ -187,8 +198,7 @@ def append_paged_kv_cache(append_key: torch.Tensor, append_value: torch.Tensor,
     ind = _i32(kv_indices, device)
     indptr = _i32(kv_indptr, device)
     bsz = indptr.numel() - 1
-    if error_flag is not None and (error_flag.dtype != torch.int32 or error_flag.numel() < 1):
-        raise ValueError("error_flag must be an int32 device tensor")
+    _check_error_flag(error_flag, 2 if paged_kv_cache.dtype == torch.float8_e4m3fn else 1)
     call("pagedattn_append_paged_kv_cache", ptr(append_key), ptr(append_value),
          append_key.stride(0), append_key.stride(1), append_value.stride(0),
          append_value.stride(1), dtype_code(append_key.dtype), ptr(bi), ptr(pos), nnz,
@@ -229,8 +239,7 @@ def rope_append_paged_kv_cache(q: torch.Tensor, append_key: torch.Tensor,
     ind = _i32(kv_indices, device)
     indptr = _i32(kv_indptr, device)
     bsz = indptr.numel() - 1
-    if error_flag is not None and (error_flag.dtype != torch.int32 or error_flag.numel() < 1):
-        raise ValueError("error_flag must be an int32 device tensor")
+    _check_error_flag(error_flag, 2 if paged_kv_cache.dtype == torch.float8_e4m3fn else 1)
     call("pagedattn_rope_append_paged_kv_cache", ptr(q), q.stride(0), q.stride(1), q.shape[1],
          ptr(append_key), ptr(append_value), append_key.stride(0), append_key.stride(1),
          append_value.stride(0), append_value.stride(1), dtype_code(append_key.dtype), ptr(bi),

@@ -83,6 +83,7 @@ Meta make_meta(double bad) {
 const char* kEnv[] = {"PAGEDATTN_DECODE_SHARED", "PAGEDATTN_DECODE_DETERMINISTIC",
                       "PAGEDATTN_DECODE_HEAD_GROUP", "PAGEDATTN_DECODE_ITEM_COST",
                       "PAGEDATTN_DECODE_WAVES_PER_CU", "PAGEDATTN_DECODE_SHARED_SLACK_KB",
+                      "PAGEDATTN_DECODE_SHARED_SLACK_PCT",
                       "PAGEDATTN_PREFILL_PAIR"};
 
 void shuffle_env() {

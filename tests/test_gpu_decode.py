@@ -327,11 +327,12 @@ def test_decode_llama3_70b_e4m3_workload(gpu):
                                         m.kv_indices, m.kv_indptr)
     assert skipped == 0
     assert np.array_equal(O.to_bits(t.pool), want)
-    # the counter at byte 0 of the workspace holds the clamped pieces
+    # the counter at byte 4 of the workspace holds the clamped pieces, the
+    # one at byte 0 the skipped tokens (none)
     clamped = O.e4m3_clamped_pieces(t.k_new.cpu().float(), t.v_new.cpu().float(),
                                     t.scales.cpu(), m.batch_indices, m.positions,
                                     m.kv_indices, m.kv_indptr, dec.num_pages)
-    assert int(ws[:4].view(torch.int32).item()) == clamped
+    assert ws[:8].view(torch.int32).tolist() == [0, clamped]
     lens = m.seq_lens
     rng = np.random.default_rng(70)
     subset = sorted(set(np.argsort(lens)[-3:].tolist()) |
@@ -403,8 +404,8 @@ def test_decode_rescale_branch(gpu, fp8, d, hq, hkv):
 def test_decode_fused_append_counts(gpu):
     # the fused e4m3 append counts what the stand-alone append counts:
     # clamped pieces (rows past +-448 x scale, a zero or infinite page
-    # scale) and new tokens outside their sequence's pages, in the int32 at
-    # byte 0 of the workspace; the pool bytes equal the oracle's
+    # scale) at byte 4 of the workspace and new tokens outside their
+    # sequence's pages at byte 0, apart; the pool bytes equal the oracle's
     d, hq, hkv = 128, 64, 8
     lens = [5, 16, 17, 40, 100, 333]
     meta, pool16, q = decode_case(gpu, lens, hq, hkv, d, seed=71)
@@ -441,4 +442,4 @@ def test_decode_fused_append_counts(gpu):
               positions=i32(pos, gpu))
         torch.cuda.synchronize()
         assert np.array_equal(O.to_bits(pb), want), split
-        assert int(ws[:4].view(torch.int32).item()) == skipped + clamped, split
+        assert ws[:8].view(torch.int32).tolist() == [skipped, clamped], split

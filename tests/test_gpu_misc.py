@@ -133,8 +133,9 @@ def test_append_e4m3_bit_exact(gpu, src):
 @pytest.mark.parametrize("with_rope", [False, True])
 def test_append_e4m3_fixed_scale_counts(gpu, src, with_rope):
     # fixed-scale e4m3 appends (stand-alone and RoPE-fused) count every
-    # skipped token and every clamped 8-element piece in error_flag; blocks
-    # with a zero or infinite scale get zero codes and are counted too
+    # skipped token in error_flag[0] and every clamped 8-element piece in
+    # error_flag[1]; blocks with a zero or infinite scale get zero codes and
+    # are counted as clamped too
     meta, pool, k, v = _append_case(gpu, src, 16, True)
     q8, scales = pagedattn.quantize_pages_e4m3(pool)
     pages = meta.kv_indices
@@ -159,7 +160,7 @@ def test_append_e4m3_fixed_scale_counts(gpu, src, with_rope):
     clamped = O.e4m3_clamped_pieces(ka.cpu().float(), v.cpu().float(), scales.cpu(), bi, pos,
                                     meta.kv_indices, meta.kv_indptr, q8.shape[0])
     assert skipped == 2 and clamped > 2 * (k.shape[2] // 8)
-    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    err = torch.zeros(2, dtype=torch.int32, device=gpu)
     args = (i32(bi, gpu), i32(pos, gpu), q8, i32(meta.kv_indices, gpu),
             i32(meta.kv_indptr, gpu), i32(meta.kv_last_page_len, gpu))
     if with_rope:
@@ -170,7 +171,7 @@ def test_append_e4m3_fixed_scale_counts(gpu, src, with_rope):
                                         error_flag=err)
     torch.cuda.synchronize()
     assert np.array_equal(O.to_bits(q8), want)
-    assert int(err.item()) == skipped + clamped
+    assert err.tolist() == [skipped, clamped]
 
 
 def _bf16_ulp(x: torch.Tensor) -> torch.Tensor:
@@ -223,14 +224,14 @@ def test_rope_append_equals_separate(gpu, dtype, prefill, fp8):
     bi[0] = 1000  # a token the append must skip (and count); RoPE still rotates it
     args = dict(kv_layout="HND", kv_scales=scales)
     q_a, k_a, pool_a = q.clone(), k.clone(), pool.clone()
-    err_a = torch.zeros(1, dtype=torch.int32, device=gpu)
+    err_a = torch.zeros(2, dtype=torch.int32, device=gpu)
     pagedattn.apply_rope_pos_ids_inplace(q_a, k_a, i32(pos, gpu), rope_theta=500000.0,
                                          rope_scale=2.0)
     pagedattn.append_paged_kv_cache(k_a, v, i32(bi, gpu), i32(pos, gpu), pool_a,
                                     i32(meta.kv_indices, gpu), i32(meta.kv_indptr, gpu),
                                     i32(meta.kv_last_page_len, gpu), error_flag=err_a, **args)
     q_b, k_b, pool_b = q.clone(), k.clone(), pool.clone()
-    err_b = torch.zeros(1, dtype=torch.int32, device=gpu)
+    err_b = torch.zeros(2, dtype=torch.int32, device=gpu)
     pagedattn.rope_append_paged_kv_cache(q_b, k_b, v, i32(bi, gpu), i32(pos, gpu), pool_b,
                                          i32(meta.kv_indices, gpu), i32(meta.kv_indptr, gpu),
                                          i32(meta.kv_last_page_len, gpu), rope_scale=2.0,
@@ -245,4 +246,4 @@ def test_rope_append_equals_separate(gpu, dtype, prefill, fp8):
     if fp8:
         clamped = O.e4m3_clamped_pieces(k_a.cpu().float(), v.cpu().float(), scales.cpu(), bi,
                                         pos, meta.kv_indices, meta.kv_indptr, pool.shape[0])
-    assert int(err_a.item()) == int(err_b.item()) == 1 + clamped
+    assert err_a.tolist() == err_b.tolist() == [1, clamped]
