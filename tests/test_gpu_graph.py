@@ -79,6 +79,79 @@ def test_build_paged_metadata_overflow_is_counted(gpu):
     assert int(err.item()) == 2
 
 
+def _meta_closed_form(tables, max_pages, lens, new_lens, idx_cap, tok_cap):
+    """The outputs and the error count of build_paged_metadata written out:
+    rows cut to max_pages pages, outputs past a capacity dropped, one count
+    per cut row and one per sequence with dropped outputs."""
+    pages = [min(-(-L // 16), max_pages) for L in lens]
+    nt = [1] * len(lens) if new_lens is None else [min(max(n, 0), max(L, 0))
+                                                   for n, L in zip(new_lens, lens)]
+    indptr = np.concatenate([[0], np.cumsum(pages)]).astype(np.int64)
+    qo = np.concatenate([[0], np.cumsum(nt)]).astype(np.int64)
+    idx = np.concatenate([np.asarray(t[:p], np.int64) for t, p in zip(tables, pages)] +
+                         [np.zeros(0, np.int64)])
+    bi = np.repeat(np.arange(len(lens)), nt)
+    pos = np.concatenate([np.arange(L - n, L) for L, n in zip(lens, nt)] + [np.zeros(0, np.int64)])
+    cut = sum(-(-L // 16) > p for L, p in zip(lens, pages))
+    dropped = sum((p > 0 and indptr[b] + p > idx_cap) or
+                  (new_lens is not None and n > 0 and qo[b] + n > tok_cap)
+                  for b, (p, n) in enumerate(zip(pages, nt)))
+    last = [(L - 1) % 16 + 1 if L > 0 else 16 for L in lens]
+    return indptr, idx, last, qo, bi, pos, cut + dropped
+
+
+@pytest.mark.parametrize("bsz", [1000, 1100])  # one launch up to 1024 sequences, two above
+@pytest.mark.parametrize("prefill", [False, True])
+def test_build_paged_metadata_large_batch(gpu, bsz, prefill):
+    """Batches on both launch shapes: equal to the host metadata rules
+    (pagedattn.metadata) when nothing is cut, and with rows cut to max_pages
+    and capacities too small, equal to the closed form with one error count
+    per cut row and per sequence with dropped outputs."""
+    rng = np.random.default_rng(bsz + prefill)
+    lens = rng.integers(1, 300, size=bsz).tolist()
+    new = rng.integers(1, 40, size=bsz).tolist() if prefill else None
+    if prefill:
+        new = [min(n, L) for n, L in zip(new, lens)]
+    tables, _ = random_tables(rng, [L + 16 for L in lens])
+    maxp = max(len(t) for t in tables)
+    bt = _tables_tensor(tables, maxp, gpu)
+    new_t = i32(new, gpu) if prefill else None
+    got = pagedattn.build_paged_metadata(bt, i32(lens, gpu), new_t)
+    want = (prefill_metadata(tables, [L - n for L, n in zip(lens, new)], new) if prefill
+            else decode_metadata(tables, lens))
+    for name in ("kv_indptr", "kv_last_page_len", "qo_indptr", "batch_indices", "positions"):
+        assert np.array_equal(getattr(got, name).cpu().numpy(), getattr(want, name)), name
+    n = int(want.kv_indptr[-1])
+    assert np.array_equal(got.kv_indices[:n].cpu().numpy(), want.kv_indices)
+
+    # cut rows (lengths past max_pages pages) and capacities below the need
+    lens2 = list(lens)
+    for b in (3, 500, bsz - 1):
+        lens2[b] = 16 * maxp + 37
+    new2 = None
+    if prefill:
+        new2 = [min(n, L) for n, L in zip(new, lens2)]
+    pages = [min(-(-L // 16), maxp) for L in lens2]
+    idx_cap = int(sum(pages) * 0.9)
+    tok_cap = int(sum(new2) * 0.8) if prefill else bsz
+    out = pagedattn.ops.new_paged_buffers(bsz, idx_cap, tok_cap, gpu)
+    err = torch.zeros(1, dtype=torch.int32, device=gpu)
+    pagedattn.build_paged_metadata(bt, i32(lens2, gpu), i32(new2, gpu) if prefill else None,
+                                   out=out, error_flag=err)
+    padded = [list(t) + [-7] * (maxp - len(t)) for t in tables]  # the table tensor's rows
+    indptr, idx, last, qo, bi, pos, count = _meta_closed_form(padded, maxp, lens2, new2,
+                                                               idx_cap, tok_cap)
+    assert np.array_equal(out.kv_indptr.cpu().numpy(), indptr)
+    assert np.array_equal(out.kv_indices.cpu().numpy(), idx[:idx_cap])
+    assert np.array_equal(out.kv_last_page_len.cpu().numpy(), last)
+    if prefill:
+        assert np.array_equal(out.qo_indptr.cpu().numpy(), qo)
+    ntok = min(tok_cap, len(bi))
+    assert np.array_equal(out.batch_indices[:ntok].cpu().numpy(), bi[:ntok])
+    assert np.array_equal(out.positions[:ntok].cpu().numpy(), pos[:ntok])
+    assert int(err.item()) == count and count > 3
+
+
 def _device_plan_run(gpu, meta, pool, q, hq, hkv, d, kv_scales=None):
     w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(workspace(gpu), "HND")
     w.plan(i32(meta.kv_indptr, gpu), i32(meta.kv_indices, gpu), i32(meta.kv_last_page_len, gpu),
