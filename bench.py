@@ -406,7 +406,7 @@ def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
     from pagedattn import workloads as W
 
     alg_step = W.decode_bytes(w, 2, with_append=True)
-    reps = _replicas(w.num_pages * 2 * w.hkv * 16 * w.d * 2, min_total=512 << 20)
+    reps = _replicas(w.num_pages * 2 * w.hkv * 16 * w.d * 2)  # as the headline step
     inst = [W.materialize(w, dev, dtype, seed=w.seed * 100 + r) for r in range(reps)]
     ws = torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
     out = torch.empty((w.meta.batch_size, w.hq, w.d), dtype=dtype, device=dev)
@@ -448,7 +448,8 @@ def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
                              steps, warmup)
     del graphs, inst
     torch.cuda.empty_cache()
-    return {"eager_ms_per_step": eager_ms, "eager_GBps": alg_step / (eager_ms * 1e-3) / 1e9,
+    return {"plan_kind": dw.plan_kind,
+            "eager_ms_per_step": eager_ms, "eager_GBps": alg_step / (eager_ms * 1e-3) / 1e9,
             "graph_ms_per_step": graph_ms, "graph_GBps": alg_step / (graph_ms * 1e-3) / 1e9,
             "graph_steps_per_graph": steps,
             "graph_one_step_ms": graph1_ms,
@@ -661,7 +662,8 @@ def main() -> int:
         extra["llama3_70b_mixed_fp8"] = c5
     if "devplan" in want:
         dp = bench_device_plan(main_w, dev, dtype)
-        log(f"tinyllama_decode (device plan): eager {dp['eager_ms_per_step'] * 1e3:.1f} us, "
+        log(f"tinyllama_decode (device plan, {dp['plan_kind']}): eager "
+            f"{dp['eager_ms_per_step'] * 1e3:.1f} us, "
             f"HIP graph {dp['graph_ms_per_step'] * 1e3:.1f} us per step")
         extra["tinyllama_decode.device_plan"] = dp
     if "kvwrite" in want:

@@ -265,10 +265,16 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
  * pagedattn_decode_plan with split_pages = 0: the (sequence, head group,
  * page) stream cut into equal shares, one share per head group of waves),
  * then merges cut sequences in a second launch over all (sequence, kv head)
- * pairs.  Both launches have fixed shapes, no host synchronisation and no
- * memsets, so a run can be captured in a HIP graph and replayed while the
- * metadata and pool change in place.  The workspace holds the split
- * partials only (2 x shares x head-group waves slots). */
+ * pairs.  When every CU would get 4 to 8 (sequence, KV head) items
+ * (4 x CUs <= batch_size x num_kv_heads <= 8 x CUs) and batch_size <= 512,
+ * the plan is a device shared-item one instead (PAGEDATTN_DECODE_SHARED=0
+ * in the environment turns that off): one launch whose workgroups (one per
+ * CU) rank the sequences by page count and take whole items, longest and
+ * shortest paired, with no split partials and no merge.  The launches have
+ * fixed shapes, no host synchronisation and no memsets, so a run can be
+ * captured in a HIP graph and replayed while the metadata and pool change
+ * in place.  The workspace holds the split partials only (2 x shares x
+ * head-group waves slots; none for a shared-item plan). */
 int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
                                  int32_t num_qo_heads, int32_t num_kv_heads,
                                  int32_t head_dim, int32_t page_size, void* workspace,
@@ -279,7 +285,9 @@ int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
  * list of head groups; sequences cut between groups are merged by a second
  * launch), PAGEDATTN_DECODE_SHARED (whole (sequence, KV head) items per
  * CU-sized workgroup whose waves share each item's pages; one launch),
- * PAGEDATTN_DECODE_DEVICE (partition made on the device at run time), or 0
+ * PAGEDATTN_DECODE_DEVICE (partition made on the device at run time),
+ * PAGEDATTN_DECODE_DEVICE_SHARED (shared-item partition dealt on the device
+ * at run time, see pagedattn_decode_plan_device), or 0
  * for a plan that is not a decode plan.  pagedattn_decode_plan with
  * split_pages = 0 takes a shared plan when its busiest CU carries at most
  * PAGEDATTN_DECODE_SHARED_SLACK_KB (environment, default 96) KiB plus
@@ -292,6 +300,7 @@ int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
 #define PAGEDATTN_DECODE_SPLIT 1
 #define PAGEDATTN_DECODE_SHARED 2
 #define PAGEDATTN_DECODE_DEVICE 3
+#define PAGEDATTN_DECODE_DEVICE_SHARED 4
 int pagedattn_decode_plan_kind(const pagedattn_plan* plan);
 
 /* BatchDecodeWithPagedKVCacheWrapper.forward(q, paged_kv_cache)

@@ -792,7 +792,88 @@ struct ChunkRef {
   int item, pg0;
 };
 
-template <int D, bool BF16, bool FP8, bool APPEND, bool ROPE>
+// Device-planned shared-item decode (DEV): the workgroup finds its items
+// itself from kv_indptr.  The B * Hkv items (sequence, KV head) are ordered
+// by the sequences' page counts, longest first (ties by index), heads in
+// order, and dealt to the n_wg workgroups in rounds of n_wg, the direction
+// alternating (round r gives workgroup w item r n_wg + w for even r, r n_wg +
+// n_wg - 1 - w for odd r), which pairs long items with short ones much as
+// the host planner's longest-first assignment does.  Every workgroup ranks
+// all sequences in its prologue (B compares of one integer key per
+// sequence, B <= kDevSharedMaxBatch), so no other launch and no host copy is
+// involved.
+// Fills L.b / h / chunk_lo / n_chunks of the workgroup's items; returns
+// their number (uniform).
+template <int D>
+__device__ __forceinline__ int dev_item_table(const DecodeParams& p, SharedLds<D>& L, int* ip,
+                                              int* lastp, int* key) {
+  const int B = p.batch_size, H = p.hkv, nwg = (int)gridDim.x, w = (int)blockIdx.x;
+  const int N = B * H;
+  if (B <= 0 || B > kDevSharedMaxBatch || N > kSharedMaxItems * nwg) {
+    // a launch the plan did not make (the host plan keeps both bounds)
+    if (threadIdx.x == 0) count_lanes(p.fault_count, true);
+    return 0;
+  }
+  int n_it = 0;
+  for (int r = 0; r < kSharedMaxItems; ++r)
+    if (r * nwg + ((r & 1) ? nwg - 1 - w : w) < N) n_it = r + 1;
+  if (n_it == 0) return 0;
+  for (int t = (int)threadIdx.x; t <= B; t += (int)blockDim.x) {
+    ip[t] = load_invariant(p.kv_indptr + t);
+    if (t < B) lastp[t] = load_invariant(p.last_page_len + t);
+  }
+  __syncthreads();
+  // one distinct key per sequence, larger for more pages, then for a smaller
+  // index (page counts capped at 2^21 for the key); -1 pads to a multiple of
+  // 16, below every key.  A sequence's rank is the number of larger keys.
+  constexpr int kKeyIdx = 1024;  // > kDevSharedMaxBatch
+  const int B16 = (B + 15) & ~15;
+  for (int t = (int)threadIdx.x; t < B16; t += (int)blockDim.x)
+    key[t] = t < B ? min(max(0, ip[t + 1] - ip[t]), (1 << 21) - 1) * kKeyIdx + (kKeyIdx - 1 - t)
+                   : -1;
+  __syncthreads();
+  for (int b = (int)threadIdx.x; b < B; b += (int)blockDim.x) {
+    const int kb = key[b];
+    int rank = 0;
+    for (int j = 0; j < B16; j += 16) {
+      const int4 v0 = *reinterpret_cast<const int4*>(key + j);
+      const int4 v1 = *reinterpret_cast<const int4*>(key + j + 4);
+      const int4 v2 = *reinterpret_cast<const int4*>(key + j + 8);
+      const int4 v3 = *reinterpret_cast<const int4*>(key + j + 12);
+      rank += (v0.x > kb) + (v0.y > kb) + (v0.z > kb) + (v0.w > kb);
+      rank += (v1.x > kb) + (v1.y > kb) + (v1.z > kb) + (v1.w > kb);
+      rank += (v2.x > kb) + (v2.y > kb) + (v2.z > kb) + (v2.w > kb);
+      rank += (v3.x > kb) + (v3.y > kb) + (v3.z > kb) + (v3.w > kb);
+    }
+    for (int hh = 0; hh < H; ++hh) {
+      const int i = rank * H + hh;
+      const int r = i / nwg, pos = i - r * nwg;
+      if (r < n_it && ((r & 1) ? nwg - 1 - pos : pos) == w) {
+        L.b[r] = b;
+        L.h[r] = hh;
+      }
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int r = 0; r < n_it; ++r) {
+      const int b = L.b[r];
+      const int np = max(0, ip[b + 1] - ip[b]);
+      const int nc = max(1, (np + 2 * kSharedStagePairs - 1) / (2 * kSharedStagePairs));
+      L.chunk_lo[r] = acc;
+      L.n_chunks[r] = nc;
+      L.ind_lo[r] = ip[b];
+      L.npages[r] = np;
+      L.last[r] = lastp[b];
+      acc += nc;
+    }
+  }
+  __syncthreads();
+  return n_it;
+}
+
+template <int D, bool BF16, bool FP8, bool APPEND, bool ROPE, bool DEV>
 __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
   using Tr = DecodeTraits<D, BF16, FP8>;
   constexpr int W = Tr::W;
@@ -806,11 +887,20 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
   const int n = lane & 15;
   const int G = lane >> 4;
   const int g = p.g;
-  const int it_lo = uniform(load_invariant(p.wave_ptr + blockIdx.x));
-  const int n_it = min(max(uniform(load_invariant(p.wave_ptr + blockIdx.x + 1)) - it_lo, 0),
-                       kSharedMaxItems);
+  int n_it;
+  const SharedItem* items = nullptr;
+  if constexpr (DEV) {
+    __shared__ int dev_ip[kDevSharedMaxBatch + 1];
+    __shared__ int dev_last[kDevSharedMaxBatch];
+    __shared__ __attribute__((aligned(16))) int dev_key[kDevSharedMaxBatch];
+    n_it = uniform(dev_item_table<D>(p, L, dev_ip, dev_last, dev_key));
+  } else {
+    const int it_lo = uniform(load_invariant(p.wave_ptr + blockIdx.x));
+    n_it = min(max(uniform(load_invariant(p.wave_ptr + blockIdx.x + 1)) - it_lo, 0),
+               kSharedMaxItems);
+    items = reinterpret_cast<const SharedItem*>(p.items) + it_lo;
+  }
   if (n_it == 0) return;  // uniform over the workgroup: no barrier is skipped by part of it
-  const SharedItem* items = reinterpret_cast<const SharedItem*>(p.items) + it_lo;
 
   // ---- item table: thread t < n_it fills item t from the plan and the
   // metadata of this launch; an item that does not match the launch keeps
@@ -819,14 +909,22 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
     const int t = threadIdx.x;
     bool skipped = false;
     if (t < n_it) {
-      const SharedItem it = items[t];
+      // the item's page range comes with it (the plan's metadata, or the
+      // kv_indptr / kv_last_page_len this launch's prologue loaded)
+      SharedItem it;
+      if constexpr (DEV) {
+        it = SharedItem{L.b[t], L.h[t], L.chunk_lo[t], L.n_chunks[t], L.ind_lo[t], L.npages[t],
+                        L.last[t], 0};
+      } else {
+        it = items[t];
+      }
       int b = it.b, h = it.h, ind_lo = 0, npages = 0, last = kPage, new_pos = -1;
-      if (b < 0 || b >= p.batch_size || h < 0 || h >= p.hkv) {
+      if (b < 0 || b >= p.batch_size || h < 0 || h >= p.hkv || it.ind_lo < 0) {
         b = -1;
       } else {
-        ind_lo = load_invariant(p.kv_indptr + b);
-        npages = max(0, load_invariant(p.kv_indptr + b + 1) - ind_lo);
-        last = min(max(load_invariant(p.last_page_len + b), 1), kPage);
+        ind_lo = it.ind_lo;
+        npages = max(0, it.npages);
+        last = min(max(it.last, 1), kPage);
         new_pos = npages > 0 ? (npages - 1) * kPage + last - 1 : -1;
         if (APPEND && p.new_pos) new_pos = load_invariant(p.new_pos + b);
         // a new token outside the sequence's pages is skipped (counted once
@@ -1245,25 +1343,29 @@ DecodeFn decode_fn_d(bool bf16, bool fp8, bool append, bool rope) {
              : decode_fn<D, false, false, IMPLICIT>(append, rope);
 }
 
-template <int D, bool BF16, bool FP8>
+template <int D, bool BF16, bool FP8, bool DEV>
 DecodeFn decode_shared_fn(bool append, bool rope) {
-  if (!append) return decode_shared_kernel<D, BF16, FP8, false, false>;
-  return rope ? decode_shared_kernel<D, BF16, FP8, true, true>
-              : decode_shared_kernel<D, BF16, FP8, true, false>;
+  if (!append) return decode_shared_kernel<D, BF16, FP8, false, false, DEV>;
+  return rope ? decode_shared_kernel<D, BF16, FP8, true, true, DEV>
+              : decode_shared_kernel<D, BF16, FP8, true, false, DEV>;
 }
 
-template <int D>
+template <int D, bool DEV>
 DecodeFn decode_shared_fn_d(bool bf16, bool fp8, bool append, bool rope) {
   if (bf16)
-    return fp8 ? decode_shared_fn<D, true, true>(append, rope)
-               : decode_shared_fn<D, true, false>(append, rope);
-  return fp8 ? decode_shared_fn<D, false, true>(append, rope)
-             : decode_shared_fn<D, false, false>(append, rope);
+    return fp8 ? decode_shared_fn<D, true, true, DEV>(append, rope)
+               : decode_shared_fn<D, true, false, DEV>(append, rope);
+  return fp8 ? decode_shared_fn<D, false, true, DEV>(append, rope)
+             : decode_shared_fn<D, false, false, DEV>(append, rope);
 }
 
-static DecodeFn pick_decode_shared(int d, bool bf16, bool fp8, bool append, bool rope) {
-  return d == 64 ? decode_shared_fn_d<64>(bf16, fp8, append, rope)
-                 : decode_shared_fn_d<128>(bf16, fp8, append, rope);
+static DecodeFn pick_decode_shared(int d, bool bf16, bool fp8, bool append, bool rope,
+                                   bool dev) {
+  if (dev)
+    return d == 64 ? decode_shared_fn_d<64, true>(bf16, fp8, append, rope)
+                   : decode_shared_fn_d<128, true>(bf16, fp8, append, rope);
+  return d == 64 ? decode_shared_fn_d<64, false>(bf16, fp8, append, rope)
+                 : decode_shared_fn_d<128, false>(bf16, fp8, append, rope);
 }
 
 static DecodeFn pick_decode(int d, bool bf16, bool fp8, bool append, bool rope, bool implicit) {
@@ -1376,7 +1478,9 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = q_dtype == PAGEDATTN_BF16;
   if (plan->shared) {
-    DecodeFn fn = pick_decode_shared(plan->d, bf16, fp8, app != nullptr, app && app->rope);
+    // a device-planned shared plan (implicit) finds its items from kv_indptr
+    DecodeFn fn = pick_decode_shared(plan->d, bf16, fp8, app != nullptr, app && app->rope,
+                                     plan->implicit);
     if (!fn)
       return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: shared-item plan for D = %d", who,
                        plan->d);

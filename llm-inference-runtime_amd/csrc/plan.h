@@ -39,9 +39,13 @@ struct PrefillItem {
 
 // One item of a shared-item decode plan (decode_shared_kernel): sequence b,
 // KV head h, its page pairs being chunks [chunk_lo, chunk_lo + n_chunks) of
-// the workgroup's chunk sequence.
+// the workgroup's chunk sequence; the sequence's pages are kv_indices
+// [ind_lo, ind_lo + npages), the last holding `last` tokens (the planned
+// metadata, which the run's is, as with FlashInfer's plan and run: the
+// kernel then reads no kv_indptr / kv_last_page_len before its first page
+// ids).
 struct SharedItem {
-  int32_t b, h, chunk_lo, n_chunks;
+  int32_t b, h, chunk_lo, n_chunks, ind_lo, npages, last, pad;
 };
 
 // Shared-item decode geometry the planner sizes its partition by: items per
@@ -49,6 +53,9 @@ struct SharedItem {
 // stage).
 constexpr int kSharedMaxItems = 8;
 constexpr int kSharedStagePairs = 1;
+// Sequences a device-planned shared-item decode ranks in every workgroup's
+// prologue (B compares per sequence).
+constexpr int kDevSharedMaxBatch = 512;
 
 // Prefill geometry: 8 waves per workgroup (two per SIMD) share every K/V tile
 // loaded into LDS, which halves the global-to-LDS traffic per MFMA against 4

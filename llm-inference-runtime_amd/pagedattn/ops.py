@@ -654,9 +654,11 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
         """The partition the current plan holds: "split" (head-group work
         list, cut sequences merged by a second launch), "shared" (whole
         (sequence, KV head) items per CU workgroup, one launch), "device"
-        (partitioned on the device at run time), or None before plan()."""
+        (split partition made on the device at run time), "device_shared"
+        (whole items dealt to the CUs on the device at run time, one launch),
+        or None before plan()."""
         k = _lib.lib().pagedattn_decode_plan_kind(self._plan.handle)
-        return {1: "split", 2: "shared", 3: "device"}.get(int(k))
+        return {1: "split", 2: "shared", 3: "device", 4: "device_shared"}.get(int(k))
 
     def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, *,
             kv_scales: torch.Tensor | None = None, out: torch.Tensor | None = None,

@@ -3,10 +3,11 @@ items per CU-sized workgroup, the four waves of the workgroup claiming the
 items' page pairs, states merged in LDS, one launch) against the fp32 CPU
 oracle, at the bounds of the bf16 and e4m3 decode tests.  The partition is
 forced with PAGEDATTN_DECODE_SHARED=1 wherever the default would not take
-it, and every test checks that the plan holds it.  Bit-for-bit comparisons
-run with PAGEDATTN_DECODE_DETERMINISTIC=1 (fixed pair assignment); by
-default pairs go to the waves in arrival order and runs agree to the last
-bits."""
+it, and every test checks that the plan holds it.  By default wave w takes
+the pairs w, w + 4, ... of its workgroup, so repeated runs are bit-identical
+(FlashInfer's decode, which this replaces, is deterministic);
+PAGEDATTN_DECODE_DETERMINISTIC=0 lets the waves claim pairs in arrival
+order, and those runs agree to the last bits."""
 
 import numpy as np
 import pytest
@@ -36,10 +37,21 @@ def shared(monkeypatch):
 
 @pytest.fixture
 def deterministic(monkeypatch):
-    # fixed chunk assignment: the states merged per item, and so the output
-    # bits, do not depend on timing (by default chunks go to the waves in
-    # arrival order)
+    # fixed chunk assignment (the default, set explicitly): the states merged
+    # per item, and so the output bits, do not depend on timing
     monkeypatch.setenv("PAGEDATTN_DECODE_DETERMINISTIC", "1")
+
+
+@pytest.fixture
+def arrival(monkeypatch):
+    # chunks claimed in arrival order through the workgroup's LDS counter
+    monkeypatch.setenv("PAGEDATTN_DECODE_DETERMINISTIC", "0")
+
+
+def _faults(ws):
+    """Merge-slot waits of shared-item runs that gave up (int32 2 of the
+    workspace header): zero in every consistent run."""
+    return int(ws[8:12].view(torch.int32).item())
 
 
 def _plan(gpu, meta, hq, hkv, d, dtype, ws=None, kind="shared"):
@@ -51,20 +63,38 @@ def _plan(gpu, meta, hq, hkv, d, dtype, ws=None, kind="shared"):
     return w
 
 
-@pytest.mark.parametrize("hq,hkv", [(32, 4), (32, 8), (8, 8), (16, 2), (64, 8), (16, 1)])
-def test_shared_edge_lengths(gpu, shared, hq, hkv):
-    meta, pool, q = decode_case(gpu, EDGE_LENS, hq, hkv, 64, seed=hq + hkv)
+@pytest.mark.parametrize("hq,hkv,d", [(32, 4, 64), (32, 8, 64), (8, 8, 64), (16, 2, 64),
+                                       (64, 8, 64), (16, 1, 64), (32, 8, 128), (64, 8, 128),
+                                       (8, 1, 128)])
+def test_shared_edge_lengths(gpu, shared, hq, hkv, d):
+    meta, pool, q = decode_case(gpu, EDGE_LENS, hq, hkv, d, seed=hq + hkv + d)
     ref_o, ref_l = oracle_decode(meta, pool, q)
-    w = _plan(gpu, meta, hq, hkv, 64, q.dtype)
+    w = _plan(gpu, meta, hq, hkv, d, q.dtype)
     out, lse = w.run(q, pool, return_lse=True)
     torch.cuda.synchronize()
     assert max_err(out, ref_o) <= TOL_BF16
     assert lse_err(lse, ref_l) <= TOL_LSE
 
 
+@pytest.mark.parametrize("hq,hkv", [(64, 8), (32, 4)])
+def test_shared_e4m3_head_dim_128(gpu, shared, hq, hkv):
+    # the 70B-shaped decode's partition: e4m3 pool at head_dim 128
+    lens = EDGE_LENS + [int(x) for x in np.random.default_rng(hq).integers(1, 3000, 40)]
+    meta, pool16, q = decode_case(gpu, lens, hq, hkv, 128, seed=hq + 1)
+    pool8, scales = pagedattn.quantize_pages_e4m3(pool16)
+    ref_o, ref_l = oracle_decode(meta, pool8, q, scales=scales)
+    ws = workspace(gpu)
+    out, lse = _plan(gpu, meta, hq, hkv, 128, q.dtype, ws=ws).run(q, pool8, kv_scales=scales,
+                                                                   return_lse=True)
+    torch.cuda.synchronize()
+    assert max_err(out, ref_o) <= TOL_FP8
+    assert lse_err(lse, ref_l) <= TOL_LSE
+    assert _faults(ws) == 0
+
+
 def test_shared_eight_items_per_workgroup(gpu, shared):
     # 2048 one-chunk items over 256 workgroups: eight items per workgroup,
-    # so states wait for their LDS slot (two slots) and every slot is reused
+    # more than the LDS slots (four at head_dim 64), so every slot is reused
     lens = [64] * 512
     meta, pool, q = decode_case(gpu, lens, 32, 4, 64, seed=7)
     ref_o, ref_l = oracle_decode(meta, pool, q)
@@ -77,19 +107,36 @@ def test_shared_eight_items_per_workgroup(gpu, shared):
 
 def test_shared_ragged_batch(gpu, shared):
     # several items of different lengths per workgroup, including items of a
-    # single chunk next to items that all four waves share
+    # single chunk next to items that all four waves share; the default
+    # assignment is fixed, so repeated runs are bit-identical
+    lens = [int(x) for x in np.random.default_rng(9).integers(1, 900, 400)]
+    meta, pool, q = decode_case(gpu, lens, 32, 4, 64, seed=9)
+    ref_o, ref_l = oracle_decode(meta, pool, q)
+    ws = workspace(gpu)
+    w = _plan(gpu, meta, 32, 4, 64, q.dtype, ws=ws)
+    out, lse = w.run(q, pool, return_lse=True)
+    torch.cuda.synchronize()
+    assert max_err(out, ref_o) <= TOL_BF16
+    assert lse_err(lse, ref_l) <= TOL_LSE
+    for _ in range(3):
+        out2, lse2 = w.run(q, pool, return_lse=True)
+        torch.cuda.synchronize()
+        assert torch.equal(out2, out)
+        assert torch.equal(lse2, lse)
+    assert _faults(ws) == 0
+
+
+def test_shared_arrival_order_runs_agree(gpu, shared, arrival):
+    # chunks claimed in arrival order: runs may differ in the last bits only
     lens = [int(x) for x in np.random.default_rng(9).integers(1, 900, 400)]
     meta, pool, q = decode_case(gpu, lens, 32, 4, 64, seed=9)
     ref_o, ref_l = oracle_decode(meta, pool, q)
     w = _plan(gpu, meta, 32, 4, 64, q.dtype)
     out, lse = w.run(q, pool, return_lse=True)
+    out2, lse2 = w.run(q, pool, return_lse=True)
     torch.cuda.synchronize()
     assert max_err(out, ref_o) <= TOL_BF16
     assert lse_err(lse, ref_l) <= TOL_LSE
-    # chunks go to the waves in arrival order, so runs may differ in the
-    # last bits only
-    out2, lse2 = w.run(q, pool, return_lse=True)
-    torch.cuda.synchronize()
     assert float((out2.float() - out.float()).abs().max()) <= 1e-2
     assert float((lse2 - lse).abs().max()) <= 1e-4
 
@@ -268,9 +315,13 @@ def test_shared_is_the_default_for_tinyllama(gpu, monkeypatch):
     assert lse_err(lse, ref_l, rows=subset) <= TOL_LSE
 
 
-def test_shared_fused_append_arrival_order(gpu, shared):
-    # default mode: the fused append writes the pool bit for bit as the
-    # stand-alone append does, and the attention agrees with the oracle
+@pytest.mark.parametrize("order", ["arrival", "fixed"])
+def test_shared_fused_append_claim_orders(gpu, shared, order, monkeypatch):
+    # both claim orders: the fused append writes the pool bit for bit as the
+    # stand-alone append does (with the fixed order each row is written by
+    # the wave that loads its page, with no barrier), and the attention
+    # agrees with the oracle
+    monkeypatch.setenv("PAGEDATTN_DECODE_DETERMINISTIC", "0" if order == "arrival" else "1")
     d, hq, hkv = 64, 32, 4
     lens = EDGE_LENS + [int(x) for x in np.random.default_rng(36).integers(1, 900, 300)]
     meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=37)

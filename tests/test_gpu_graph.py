@@ -249,10 +249,14 @@ class _Step:
                    rope=(1.0, 5e5), positions=self.buf.positions)
 
 
-def test_decode_step_graph_replay(gpu):
+@pytest.mark.parametrize("bsz,hq,hkv,d,kind", [
+    (48, 32, 8, 128, "device"),           # 384 items: the split device partition
+    (128, 32, 8, 128, "device_shared"),   # 1024 items: whole items dealt on the device
+    (256, 32, 4, 64, "device_shared"),    # the TinyLlama batch shape
+])
+def test_decode_step_graph_replay(gpu, bsz, hq, hkv, d, kind):
     rng = np.random.default_rng(11)
-    hq, hkv, d = 32, 8, 128
-    start = [int(x) for x in rng.integers(1, 3000, 48)]
+    start = [int(x) for x in rng.integers(1, 3000, bsz)]
     start[0], start[1] = 15, 16  # crosses a page boundary in the first replays
     steps = 6
     tables, num_pages = random_tables(rng, [n + steps for n in start], extra_pages=2)
@@ -263,6 +267,7 @@ def test_decode_step_graph_replay(gpu):
     pool_e = pool_g.clone()
     eager = _Step(gpu, tables, maxp, hq, hkv, d, graph=False)
     graphed = _Step(gpu, tables, maxp, hq, hkv, d, graph=True)
+    assert eager.w.plan_kind == graphed.w.plan_kind == kind
     lens0 = torch.tensor(start, dtype=torch.int32, device=gpu)
     graphed.lens.copy_(lens0)
     # warm up on a side stream, as torch asks before a capture
@@ -305,3 +310,42 @@ def test_decode_step_graph_replay(gpu):
                                    rope_scale=1.0, rope_theta=5e5)
     ref, _ = oracle_decode(meta, pool_e, qr, batch=rows)
     assert max_err(eager.out, ref, rows) < 2e-2
+
+
+@pytest.mark.parametrize("name,lens,hq,hkv,d,fp8", [
+    ("tinyllama", list(np.random.default_rng(21).integers(1, 2049, 300)), 32, 4, 64, False),
+    ("empties", [0, 0, 3] + list(np.random.default_rng(22).integers(1, 700, 260)) + [0],
+     32, 4, 64, False),
+    ("skewed", [60000] + list(np.random.default_rng(23).integers(1, 300, 300)), 16, 4, 64, False),
+    ("e4m3_d128", list(np.random.default_rng(24).integers(1, 8193, 128)), 64, 8, 128, True),
+    ("bf16_d128", list(np.random.default_rng(25).integers(1, 3000, 160)), 32, 8, 128, False),
+])
+def test_device_shared_plan(gpu, name, lens, hq, hkv, d, fp8):
+    """The device-dealt shared-item partition: one launch, repeated runs
+    bit-identical, outputs and lse against the oracle, faults counter zero."""
+    lens = [int(x) for x in lens]
+    meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=len(lens) + 3)
+    scales = None
+    if fp8:
+        pool, scales = pagedattn.quantize_pages_e4m3(pool)
+    ws = workspace(gpu)
+    w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    w.plan(i32(meta.kv_indptr, gpu), i32(meta.kv_indices, gpu), i32(meta.kv_last_page_len, gpu),
+           hq, hkv, d, 16, q_data_type=q.dtype, device_plan=True)
+    assert w.plan_kind == "device_shared"
+    out, lse = w.run(q, pool, kv_scales=scales, return_lse=True)
+    out2, lse2 = w.run(q, pool, kv_scales=scales, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    assert int(ws[8:12].view(torch.int32).item()) == 0
+    rows = sorted({0, len(lens) - 1, int(np.argmax(lens)), int(np.argmin(lens))} |
+                  set(range(1, len(lens), max(1, len(lens) // 12))))
+    rows = [b for b in rows if 0 < lens[b] <= 20000] + ([int(np.argmax(lens))]
+                                                         if name == "skewed" else [])
+    ref, ref_lse = oracle_decode(meta, pool, q, batch=rows, scales=scales)
+    tol = 3e-2 if fp8 else 2e-2
+    assert max_err(out, ref, rows) <= tol
+    assert lse_err(lse, ref_lse, rows) <= 2e-3
+    for b in range(len(lens)):
+        if lens[b] == 0:
+            assert torch.all(out[b] == 0) and torch.all(torch.isinf(lse[b]))
