@@ -770,6 +770,7 @@ constexpr int kSharedSpinLimit = 1 << 24;
 
 template <int D>
 struct SharedLds {
+  int n_it;       // items of the workgroup
   int total;      // chunks of the workgroup's items
   int next;       // chunk counter (claims in arrival order)
   static constexpr int S = shared_slots<D>();
@@ -887,37 +888,39 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
   const int n = lane & 15;
   const int G = lane >> 4;
   const int g = p.g;
-  int n_it;
-  const SharedItem* items = nullptr;
+  int n_it = 0;
   if constexpr (DEV) {
     __shared__ int dev_ip[kDevSharedMaxBatch + 1];
     __shared__ int dev_last[kDevSharedMaxBatch];
     __shared__ __attribute__((aligned(16))) int dev_key[kDevSharedMaxBatch];
     n_it = uniform(dev_item_table<D>(p, L, dev_ip, dev_last, dev_key));
-  } else {
-    const int it_lo = uniform(load_invariant(p.wave_ptr + blockIdx.x));
-    n_it = min(max(uniform(load_invariant(p.wave_ptr + blockIdx.x + 1)) - it_lo, 0),
-               kSharedMaxItems);
-    items = reinterpret_cast<const SharedItem*>(p.items) + it_lo;
+    if (n_it == 0) return;  // uniform over the workgroup: no barrier is skipped by part of it
   }
-  if (n_it == 0) return;  // uniform over the workgroup: no barrier is skipped by part of it
 
   // ---- item table: thread t < n_it fills item t from the plan and the
   // metadata of this launch; an item that does not match the launch keeps
-  // its chunks but reads and writes nothing (b = -1, no pages)
+  // its chunks but reads and writes nothing (b = -1, no pages).  A host
+  // plan's workgroup reads its kSharedMaxItems entries at once (fixed
+  // stride), every entry carrying the workgroup's item count.
   {
     const int t = threadIdx.x;
     bool skipped = false;
-    if (t < n_it) {
+    SharedItem it{-1, 0, 0, 0, -1, 0, kPage, 0};
+    int cnt = n_it;
+    if constexpr (DEV) {
+      if (t < n_it)
+        it = SharedItem{L.b[t], L.h[t], L.chunk_lo[t], L.n_chunks[t], L.ind_lo[t], L.npages[t],
+                        L.last[t], n_it};
+    } else {
+      if (t < kSharedMaxItems) {
+        it = reinterpret_cast<const SharedItem*>(p.items)[(int64_t)blockIdx.x * kSharedMaxItems + t];
+        cnt = min(max(it.wg_items, 0), kSharedMaxItems);
+        if (t == 0) L.n_it = cnt;
+      }
+    }
+    if (t < cnt) {
       // the item's page range comes with it (the plan's metadata, or the
       // kv_indptr / kv_last_page_len this launch's prologue loaded)
-      SharedItem it;
-      if constexpr (DEV) {
-        it = SharedItem{L.b[t], L.h[t], L.chunk_lo[t], L.n_chunks[t], L.ind_lo[t], L.npages[t],
-                        L.last[t], 0};
-      } else {
-        it = items[t];
-      }
       int b = it.b, h = it.h, ind_lo = 0, npages = 0, last = kPage, new_pos = -1;
       if (b < 0 || b >= p.batch_size || h < 0 || h >= p.hkv || it.ind_lo < 0) {
         b = -1;
@@ -940,7 +943,7 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
       L.npages[t] = npages;
       L.last[t] = last;
       L.new_pos[t] = new_pos;
-      if (t == n_it - 1) L.total = it.chunk_lo + max(it.n_chunks, 0);
+      if (t == cnt - 1) L.total = it.chunk_lo + max(it.n_chunks, 0);
     }
     if (t == 0) L.next = 0;
     if (t < SharedLds<D>::S) {
@@ -951,6 +954,10 @@ __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
     if constexpr (APPEND) count_lanes(p.append_err, skipped);
   }
   __syncthreads();
+  if constexpr (!DEV) {
+    n_it = uniform(L.n_it);
+    if (n_it == 0) return;  // uniform over the workgroup: no barrier is skipped by part of it
+  }
 
   // the table in lanes: lane i < n_it holds item i's fields
   const int li = lane < n_it ? lane : 0;

@@ -99,8 +99,7 @@ static int decode_shared_slack_pct() {
 // when the busiest workgroup exceeds the mean by more than the slack.
 static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_indptr_host,
                         const int32_t* kv_last_page_len_host, int hkv, int d, int cus,
-                        bool forced, std::vector<SharedItem>* items,
-                        std::vector<int32_t>* wg_ptr) {
+                        bool forced, std::vector<SharedItem>* items, int* n_wg_out) {
   const int batch = (int)npages.size();
   const int64_t n_all = (int64_t)batch * hkv;
   if (n_all == 0) return false;
@@ -139,20 +138,24 @@ static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_in
                      decode_shared_slack_bytes() * n_wg * 100 +
                          sum * page_bytes * decode_shared_slack_pct())
     return false;
-  items->clear();
-  wg_ptr->assign(1, 0);
+  // fixed stride: workgroup w's items at [w kSharedMaxItems, ...), padded
+  items->assign((size_t)n_wg * kSharedMaxItems, SharedItem{-1, 0, 0, 0, -1, 0, kPage, 0});
   for (int w = 0; w < n_wg; ++w) {
     int32_t chunk = 0;
-    for (int32_t id : per[w]) {
+    const int32_t cnt = (int32_t)per[w].size();
+    SharedItem* at = items->data() + (size_t)w * kSharedMaxItems;
+    for (int k = 0; k < kSharedMaxItems; ++k) at[k].wg_items = cnt;
+    for (int k = 0; k < cnt; ++k) {
+      const int32_t id = per[w][k];
       const int32_t np = npages[id / hkv];
       const int32_t nc = std::max<int32_t>(1, ((np + 1) / 2 + chunk_pages / 2 - 1) / (chunk_pages / 2));
       const int b = id / hkv;
-      items->push_back(SharedItem{b, id % hkv, chunk, nc, kv_indptr_host[b], np,
-                                  np > 0 ? kv_last_page_len_host[b] : kPage, 0});
+      at[k] = SharedItem{b, id % hkv, chunk, nc, kv_indptr_host[b], np,
+                         np > 0 ? kv_last_page_len_host[b] : kPage, cnt};
       chunk += nc;
     }
-    wg_ptr->push_back((int32_t)items->size());
   }
+  *n_wg_out = n_wg;
   return true;
 }
 
@@ -245,18 +248,15 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
 
   if (split_pages == 0 && decode_shared_mode() != 0) {
     std::vector<SharedItem> sitems;
-    std::vector<int32_t> wg_ptr;
+    int n_wg = 0;
     if (plan_shared(npages, kv_indptr_host, kv_last_page_len_host, hkv, head_dim, cus,
-                    decode_shared_mode() == 1, &sitems, &wg_ptr)) {
-      const int n_wg = (int)wg_ptr.size() - 1;
+                    decode_shared_mode() == 1, &sitems, &n_wg)) {
       const size_t off_items = kWsHeader;
-      const size_t off_wg = ws_align(off_items + sizeof(SharedItem) * sitems.size());
-      const size_t end = ws_align(off_wg + sizeof(int32_t) * wg_ptr.size());
+      const size_t end = ws_align(off_items + sizeof(SharedItem) * sitems.size());
       const size_t host_bytes = end - kWsHeader;
       plan->host.assign(host_bytes / sizeof(int32_t), 0);
       char* hb = reinterpret_cast<char*>(plan->host.data());
       std::memcpy(hb, sitems.data(), sizeof(SharedItem) * sitems.size());
-      std::memcpy(hb + (off_wg - kWsHeader), wg_ptr.data(), sizeof(int32_t) * wg_ptr.size());
       plan->workspace = workspace;
       plan->workspace_bytes = workspace_bytes;
       rc = upload_plan(plan, who, host_bytes, end, stream);
@@ -276,7 +276,7 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
       plan->n_slots = 0;
       plan->split_pages = split_pages;
       plan->items_dev = ws + off_items;
-      plan->wave_ptr_dev = reinterpret_cast<const int32_t*>(ws + off_wg);
+      plan->wave_ptr_dev = nullptr;
       plan->merge_dev = nullptr;
       plan->partial_o = nullptr;
       plan->partial_lse = nullptr;

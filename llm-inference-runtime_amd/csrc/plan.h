@@ -43,9 +43,12 @@ struct PrefillItem {
 // [ind_lo, ind_lo + npages), the last holding `last` tokens (the planned
 // metadata, which the run's is, as with FlashInfer's plan and run: the
 // kernel then reads no kv_indptr / kv_last_page_len before its first page
-// ids).
+// ids).  Workgroup w's items are entries [w kSharedMaxItems, (w + 1)
+// kSharedMaxItems) of the list, each carrying the workgroup's item count in
+// wg_items (entries past it are padding), so the kernel's first load is its
+// items themselves.
 struct SharedItem {
-  int32_t b, h, chunk_lo, n_chunks, ind_lo, npages, last, pad;
+  int32_t b, h, chunk_lo, n_chunks, ind_lo, npages, last, wg_items;
 };
 
 // Shared-item decode geometry the planner sizes its partition by: items per
