@@ -333,6 +333,21 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
     st_step = _stats(time_steps(step, args.steps, args.warmup))
     st = _stats(time_steps(attn, args.steps, args.warmup))
     ms = st["ms_median"]
+    # the same attention with the q-tile list cut on the device by every run
+    # (pagedattn_prefill_plan_device: a one-workgroup plan launch ahead of
+    # the attention), eagerly and `steps` runs replayed from one HIP graph
+    ws_dev = torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
+    pd = pagedattn.BatchPrefillWithPagedKVCacheWrapper(ws_dev, "HND")
+    pd.plan(t0.qo_indptr, t0.kv_indptr, t0.kv_indices, t0.kv_last_page_len, w.hq, w.hkv, w.d,
+            16, q_data_type=dtype, causal=True, device_plan=True, max_qo_tokens=int(w.meta.nnz))
+
+    def attn_dev(i):
+        t = inst[i % reps]
+        pd.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps])
+
+    dev_ms = _stats(time_steps(attn_dev, args.steps, args.warmup))["ms_median"]
+    dev_graph_ms = _time_graph_ms(attn_dev, args.steps, args.warmup)
+    dropped = int(ws_dev[12:16].view(torch.int32).item())
     res = {
         "workload": label,
         **{k: round(v, 5) if isinstance(v, float) else v for k, v in st.items()},
@@ -342,12 +357,17 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         "rows": int(w.meta.nnz),
         "kv_tokens": int(w.meta.seq_lens.sum()),
         "replicas": reps,
+        "device_plan": {"attn_ms_median": round(dev_ms, 5),
+                        "attn_TFLOPs": flops / (dev_ms * 1e-3) / 1e12,
+                        "graph_ms_per_run": round(dev_graph_ms, 5),
+                        "graph_TFLOPs": flops / (dev_graph_ms * 1e-3) / 1e12,
+                        "dropped_tiles": dropped},
     }
     res["frac"] = res["attn_TFLOPs"] / BF16_PEAK_TFLOPS
     res["roofline"] = roofline("mfma", kernel, res["attn_TFLOPs"], flops, ms, label)
     if cpu_seqs is not None:
         res["cpu_baseline"] = cpu_prefill_baseline(w, inst[0], cpu_seqs)
-    del inst, outs
+    del inst, outs, ws_dev
     torch.cuda.empty_cache()
     return res
 
@@ -625,7 +645,9 @@ def main() -> int:
         pr = bench_prefill(pw, sub, dev, dtype, "llama3_8b_prefill",
                            list(range(pw.meta.batch_size)) if cpu else None, PREFILL_KERNEL["c3"])
         log(f"llama3_8b_prefill: {pr['ms_median'] * 1e3:.1f} us = {pr['attn_TFLOPs']:.1f} "
-            f"TFLOP/s ({100 * pr['frac']:.1f}% of bf16 peak)")
+            f"TFLOP/s ({100 * pr['frac']:.1f}% of bf16 peak); device plan "
+            f"{pr['device_plan']['attn_ms_median'] * 1e3:.1f} us eager, "
+            f"{pr['device_plan']['graph_ms_per_run'] * 1e3:.1f} us from a graph")
         extra["llama3_8b_prefill"] = pr
     if "c4" in want or "c4b" in want:
         lw = W.llama3_8b_long_decode(seed=args.seed)

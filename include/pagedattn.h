@@ -240,11 +240,13 @@ int pagedattn_build_paged_metadata(const int32_t* block_tables, int64_t table_st
  * The work list and split partials are placed in `workspace` (device,
  * 256-byte aligned, workspace_bytes long) from byte 256 on, with one
  * hipMemcpyAsync on `stream`.  Bytes [0, 256) are the caller's, except
- * three int32 counters that runs increment and the library never clears:
+ * four int32 counters that runs increment and the library never clears:
  * byte 0, tokens the fused-append decode runs skipped; byte 4, e4m3 pieces
  * they clamped; byte 8, merge-slot waits of a shared-item decode run that
  * gave up (never in a consistent run: the item's output is then left
- * unwritten rather than merged wrongly). */
+ * unwritten rather than merged wrongly); byte 12, q-tiles that device-planned
+ * prefill runs dropped because they exceeded the plan's capacity (their
+ * output rows are left unwritten). */
 pagedattn_plan* pagedattn_plan_create(void);
 void pagedattn_plan_destroy(pagedattn_plan* plan);
 
@@ -258,7 +260,7 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
 
 /* Decode plan that reads no metadata on the host: the
  * BatchDecodeWithPagedKVCacheWrapper(use_cuda_graph=True) counterpart of
- * begin_forward (src/models/llama.py:133-147; the reference's todo.md:14
+ * begin_forward (src/models/llama.py:133-147; the reference's todo.md:15
  * asks for CUDA-graph decode).  Only the batch size and head shape are
  * fixed here; every pagedattn_decode_run* with this plan partitions the
  * work on the device from the kv_indptr it is given (the balanced split of
@@ -379,6 +381,25 @@ int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
                            int32_t num_kv_heads, int32_t head_dim,
                            int32_t page_size, void* workspace,
                            size_t workspace_bytes, void* stream);
+
+/* Prefill plan that reads no metadata on the host, for a chunked-prefill
+ * step captured in a HIP graph (the reference plans every step on the host,
+ * src/models/llama.py:86-116; its todo.md:15 asks for CUDA graphs).  Only
+ * the batch size, head shape and a bound on the query tokens of a run
+ * (max_qo_tokens, the sum of the qo lengths) are fixed here.  Every
+ * pagedattn_prefill_run with this plan first launches one workgroup that
+ * cuts the q-tiles of the run's qo_indptr / kv_indptr / kv_last_page_len
+ * exactly as pagedattn_prefill_plan does (same pairing, up to 1024 tiles
+ * ordered longest first), into the workspace, then the attention over the
+ * plan's fixed capacity of ceil(max_qo_tokens / q_tile) + batch_size tiles;
+ * entries past the run's tiles return at once.  The outputs equal those of
+ * a host plan bit for bit.  Tiles beyond the capacity (a run with more than
+ * max_qo_tokens query tokens) are skipped and counted at byte 12 of the
+ * workspace.  batch_size <= 4096. */
+int pagedattn_prefill_plan_device(pagedattn_plan* plan, int32_t batch_size,
+                                  int32_t num_qo_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t page_size, int64_t max_qo_tokens,
+                                  void* workspace, size_t workspace_bytes);
 
 /* BatchPrefillWithPagedKVCacheWrapper.forward(q, paged_kv_cache, causal)
  * (src/models/llama.py:212-228).  Ragged q [nnz, num_qo_heads, head_dim];

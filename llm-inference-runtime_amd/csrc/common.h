@@ -225,4 +225,31 @@ __device__ __forceinline__ float sum_over_groups16(float v) {
   return v;
 }
 
+// Exclusive prefix sum of v over the THREADS threads of the workgroup (every
+// thread calls it); *total gets the sum.  `red` holds THREADS / 64 wave
+// totals in LDS.
+template <int THREADS>
+__device__ __forceinline__ int block_excl_scan(int v, int* total, int* red) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == kWave - 1) red[wave] = x;
+  __syncthreads();
+  int before = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < THREADS / kWave; ++w) {
+    const int t = red[w];
+    before += w < wave ? t : 0;
+    all += t;
+  }
+  __syncthreads();
+  *total = all;
+  return before + x - v;
+}
+
 }  // namespace pa

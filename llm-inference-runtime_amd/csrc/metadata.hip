@@ -58,31 +58,6 @@ __device__ __forceinline__ bool seq_dropped(const MetaArgs& a, int off, int np, 
   return pages || toks;
 }
 
-// Exclusive prefix sum over the 1024 threads of the workgroup; *total gets
-// the sum.  `red` holds 16 wave totals.
-__device__ __forceinline__ int block_excl_scan(int v, int* total, int* red) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x >> 6;
-  int x = v;
-#pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) {
-    const int y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
-  if (lane == kWave - 1) red[wave] = x;
-  __syncthreads();
-  int before = 0, all = 0;
-#pragma unroll
-  for (int w = 0; w < kMetaThreads / kWave; ++w) {
-    const int t = red[w];
-    before += w < wave ? t : 0;
-    all += t;
-  }
-  __syncthreads();
-  *total = all;
-  return before + x - v;
-}
-
 // One workgroup: page and token offsets of every sequence, last page
 // lengths, and (decode) the token -> sequence / position rows.
 __global__ void __launch_bounds__(kMetaThreads) meta_scan_kernel(MetaArgs a) {
@@ -97,8 +72,8 @@ __global__ void __launch_bounds__(kMetaThreads) meta_scan_kernel(MetaArgs a) {
     const int nt = b < a.batch ? seq_new_tokens(a, b, L) : 0;
     clipped += full > np ? 1 : 0;
     int tot_p, tot_t;
-    const int ep = block_excl_scan(np, &tot_p, red[0]);
-    const int et = block_excl_scan(nt, &tot_t, red[1]);
+    const int ep = block_excl_scan<kMetaThreads>(np, &tot_p, red[0]);
+    const int et = block_excl_scan<kMetaThreads>(nt, &tot_t, red[1]);
     if (b < a.batch) {
       a.kv_indptr[b] = run_pages + ep;
       if (a.qo_indptr) a.qo_indptr[b] = run_tokens + et;

@@ -66,6 +66,11 @@ constexpr int kDevSharedMaxBatch = 512;
 constexpr int kPrefillWaves = 8;
 constexpr int kPrefillRB = 1;
 constexpr int kPrefillRows = kPrefillWaves * 32 * kPrefillRB;
+// Device-planned prefill: sequences a plan may hold (the plan kernel's
+// workgroup scans four per thread) and q-tiles it orders longest first
+// (one rank each per thread; beyond this the tiles keep sequence order).
+constexpr int kPrefillDevMaxBatch = 4096;
+constexpr int kPrefillDevSortMax = 1024;
 
 // Workspace layout: [0, kWsHeader) is reserved for the caller's device flags
 // (the Python shim keeps the append error counter at offset 0).
@@ -84,7 +89,9 @@ struct pagedattn_plan {
   // decode: log2 of the waves (KV heads) per head group
   int hg_shift = 0;
   // decode: the partition is made on the device at run time from kv_indptr
-  // (n_items = number of shares); no work list in the workspace
+  // (n_items = number of shares); no work list in the workspace.
+  // prefill: the q-tile list is built on the device at run time from
+  // qo_indptr (n_items = its capacity)
   bool implicit = false;
   // decode, implicit: page-equivalents charged per (sequence, head group)
   // segment by the device-side split
@@ -96,6 +103,9 @@ struct pagedattn_plan {
   bool deterministic = false;
   // prefill: query tokens per tile (rows = tokens * hq/hkv)
   int q_tile = 0;
+  // prefill: tiles of at most half a workgroup's rows run as KV-head pairs
+  // (device plans apply it at run time; host plans flag their items)
+  bool prefill_pair = false;
   int64_t total_qo = 0;
   // device pointers into the workspace
   void* items_dev = nullptr;

@@ -626,6 +626,112 @@ static PrefillFn pick_prefill(int d, bool bf16, bool fp8) {
   return fp8 ? prefill_fn<128, false, true>() : prefill_fn<128, false, false>();
 }
 
+// ----------------------------------------------------------------------------
+// Device plan (pagedattn_prefill_plan_device): one workgroup builds the
+// q-tile list that pagedattn_prefill_plan builds on the host, from the
+// qo_indptr / kv_indptr / kv_last_page_len of the run, so a prefill step
+// needs no host copy of its metadata and can be captured in a HIP graph.
+// Tiles are cut per sequence exactly as the host planner cuts them; up to
+// kPrefillDevSortMax tiles are ordered by the kv tokens their last row sees,
+// longest first (ties in sequence order, as the host's stable sort), more
+// keep sequence order.  The order only schedules the workgroups: every
+// tile's output is the same wherever it runs.  Entries past the tiles, up to
+// the plan's capacity, get b = -1 (the attention workgroups return at once);
+// tiles beyond the capacity are dropped and counted in `dropped`.
+struct PrefillPlanArgs {
+  const int32_t* qo_indptr;
+  const int32_t* kv_indptr;
+  const int32_t* last_page_len;
+  int32_t batch_size, q_tile, g, pair, cap;
+  PrefillItem* items;
+  int32_t* dropped;
+};
+
+constexpr int kPrefillPlanThreads = 1024;
+
+__global__ void __launch_bounds__(kPrefillPlanThreads) prefill_plan_kernel(PrefillPlanArgs a) {
+  static_assert(kPrefillDevMaxBatch <= 4 * kPrefillPlanThreads, "four sequences per thread");
+  static_assert(kPrefillDevSortMax <= kPrefillPlanThreads, "one sorted tile per thread");
+  __shared__ int start[kPrefillDevMaxBatch + 1];  // first tile of each sequence
+  __shared__ int red[kPrefillPlanThreads / kWave];
+  __shared__ long long key[kPrefillDevSortMax];
+  const int t = threadIdx.x;
+  const int B = min(max(a.batch_size, 0), kPrefillDevMaxBatch);
+  auto qo_len = [&](int b) {
+    return (int)min<int64_t>(max<int64_t>((int64_t)a.qo_indptr[b + 1] - a.qo_indptr[b], 0),
+                             INT_MAX);
+  };
+  // tiles of sequences 4t .. 4t + 3, each clamped to cap + 1 so that the
+  // sums stay in int32 and a too-large total is still seen as one
+  int c[4];
+  int mine = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int b = 4 * t + k;
+    int n = 0;
+    if (b < B) {
+      const int qo = qo_len(b);
+      n = (int)min<int64_t>(((int64_t)qo + a.q_tile - 1) / a.q_tile, (int64_t)a.cap + 1);
+    }
+    c[k] = n;
+    mine += n;
+  }
+  int total = 0;
+  int run = block_excl_scan<kPrefillPlanThreads>(mine, &total, red);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int b = 4 * t + k;
+    if (b <= B) start[b] = run;
+    run += c[k];
+  }
+  __syncthreads();
+  const int n_tiles = min(total, a.cap);
+  if (t == 0 && total > a.cap && a.dropped) atomicAdd(a.dropped, total - a.cap);
+  // tile i: the last sequence whose first tile is <= i (sequences without
+  // tiles share their successor's start and are passed over)
+  auto tile = [&](int i, int64_t* cost) {
+    int lo = 0, hi = B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (start[mid] <= i) lo = mid;
+      else hi = mid - 1;
+    }
+    const int b = lo;
+    const int qo = qo_len(b);
+    const int q_lo = (i - start[b]) * a.q_tile;  // < qo
+    const int q_hi = qo - q_lo > a.q_tile ? q_lo + a.q_tile : qo;
+    if (cost) {
+      const int np = max(a.kv_indptr[b + 1] - a.kv_indptr[b], 0);
+      const int last = min(max(a.last_page_len[b], 1), kPage);
+      const int64_t kv_len = np > 0 ? (int64_t)(np - 1) * kPage + last : 0;
+      *cost = max<int64_t>(0, min<int64_t>(kv_len, kv_len - qo + q_hi));
+    }
+    const int flag = a.pair && (int64_t)(q_hi - q_lo) * a.g <= kPrefillRows / 2 ? 1 : -1;
+    return PrefillItem{b, q_lo, q_hi, flag};
+  };
+  if (n_tiles <= kPrefillDevSortMax) {
+    // one tile per thread; its rank among unique keys (cost, then sequence
+    // order) is its place in the list
+    PrefillItem it{-1, 0, 0, -1};
+    if (t < n_tiles) {
+      int64_t cost = 0;
+      it = tile(t, &cost);
+      key[t] = (cost << 10) | (kPrefillDevSortMax - 1 - t);
+    }
+    __syncthreads();
+    if (t < n_tiles) {
+      const long long mk = key[t];
+      int rank = 0;
+      for (int j = 0; j < n_tiles; ++j) rank += key[j] > mk ? 1 : 0;
+      a.items[rank] = it;
+    }
+  } else {
+    for (int i = t; i < n_tiles; i += kPrefillPlanThreads) a.items[i] = tile(i, nullptr);
+  }
+  for (int i = n_tiles + t; i < a.cap; i += kPrefillPlanThreads)
+    a.items[i] = PrefillItem{-1, 0, 0, -1};
+}
+
 }  // namespace pa
 
 using namespace pa;
@@ -661,6 +767,9 @@ int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
     return set_error(PAGEDATTN_ERR_UNSUPPORTED,
                      "%s: sm_scale must be a positive finite number", who);
   if (plan->n_items == 0) return PAGEDATTN_OK;
+  if (plan->implicit && plan->batch_size > kPrefillDevMaxBatch)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: device plan of %d sequences", who,
+                     plan->batch_size);
   if ((int64_t)plan->n_items * plan->hkv > INT32_MAX)
     return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: too many work items", who);
   if (!q || !qo_indptr || !paged_kv_cache || !kv_indices || !kv_indptr ||
@@ -697,6 +806,17 @@ int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
   p.causal = causal ? 1 : 0;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   PrefillFn fn = pick_prefill(plan->d, q_dtype == PAGEDATTN_BF16, fp8);
+  if (plan->implicit) {
+    // the work list of this run, built on the device ahead of the attention
+    PrefillPlanArgs a{qo_indptr, kv_indptr, kv_last_page_len, plan->batch_size,
+                      plan->q_tile, p.g, plan->prefill_pair ? 1 : 0, plan->n_items,
+                      static_cast<PrefillItem*>(plan->items_dev),
+                      reinterpret_cast<int32_t*>(static_cast<char*>(plan->workspace) + 12)};
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPrefillPlanThreads), 0,
+                       (hipStream_t)stream, a);
+    int rc = check_launch(who);
+    if (rc) return rc;
+  }
   hipLaunchKernelGGL(fn, dim3(plan->n_items * plan->hkv), dim3(64 * kPrefillWaves), 0,
                      (hipStream_t)stream, p);
   return check_launch(who);

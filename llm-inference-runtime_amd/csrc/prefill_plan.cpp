@@ -1,6 +1,8 @@
 // Prefill planning on the host (BatchPrefillWithPagedKVCacheWrapper.plan,
 // src/models/llama.py:86-116): the q-tile work list of
-// pagedattn_prefill_plan.  Plain host C++ (no device code), so the planner
+// pagedattn_prefill_plan, and the fixed shapes of a device plan
+// (pagedattn_prefill_plan_device), whose list prefill.hip's plan kernel
+// builds at run time.  Plain host C++ (no device code), so the planner
 // can also be built and driven on a machine without a GPU, under the
 // address and undefined-behaviour sanitizers.
 #include <algorithm>
@@ -113,6 +115,56 @@ int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
   plan->q_tile = q_tile;
   plan->total_qo =
       batch_size > 0 ? (int64_t)qo_indptr_host[batch_size] - qo_indptr_host[0] : 0;
+  plan->items_dev = static_cast<char*>(workspace) + kWsHeader;
+  plan->implicit = false;
+  plan->shared = false;
+  plan->mode = kPlanPrefill;
+  return PAGEDATTN_OK;
+}
+
+int pagedattn_prefill_plan_device(pagedattn_plan* plan, int32_t batch_size,
+                                  int32_t num_qo_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t page_size, int64_t max_qo_tokens,
+                                  void* workspace, size_t workspace_bytes) {
+  const char* who = "prefill_plan_device";
+  if (!plan) return set_error(PAGEDATTN_ERR_INVALID, "%s: null plan", who);
+  plan->mode = kPlanNone;
+  if (batch_size < 0 || batch_size > kPrefillDevMaxBatch)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: batch_size %d outside [0, %d]", who,
+                     batch_size, kPrefillDevMaxBatch);
+  if (max_qo_tokens < 0)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: max_qo_tokens %lld < 0", who,
+                     (long long)max_qo_tokens);
+  int rc = validate_heads(who, num_qo_heads, num_kv_heads, head_dim, page_size);
+  if (rc) return rc;
+  if (!workspace || ((uintptr_t)workspace & (kWsAlign - 1)))
+    return set_error(PAGEDATTN_ERR_INVALID,
+                     "%s: workspace must be a 256-byte aligned device buffer", who);
+  const int g = num_qo_heads / num_kv_heads;
+  const int q_tile = kPrefillRows / g;
+  // every sequence may end in a partial tile
+  const int64_t cap = (max_qo_tokens + q_tile - 1) / q_tile + batch_size;
+  if ((int64_t)sizeof(PrefillItem) * cap > (int64_t)workspace_bytes - (int64_t)kWsHeader ||
+      cap * num_kv_heads > INT32_MAX)
+    return set_error(PAGEDATTN_ERR_WORKSPACE,
+                     "%s: %lld q-tiles do not fit the %zu-byte workspace", who,
+                     (long long)cap, workspace_bytes);
+  plan->host.clear();
+  plan->workspace = workspace;
+  plan->workspace_bytes = workspace_bytes;
+  plan->implicit = true;
+  plan->shared = false;
+  plan->prefill_pair = prefill_pairing() && num_kv_heads % 2 == 0;
+  plan->batch_size = batch_size;
+  plan->hq = num_qo_heads;
+  plan->hkv = num_kv_heads;
+  plan->d = head_dim;
+  plan->page_size = page_size;
+  plan->n_items = (int)cap;
+  plan->n_merge = 0;
+  plan->n_slots = 0;
+  plan->q_tile = q_tile;
+  plan->total_qo = max_qo_tokens;
   plan->items_dev = static_cast<char*>(workspace) + kWsHeader;
   plan->mode = kPlanPrefill;
   return PAGEDATTN_OK;

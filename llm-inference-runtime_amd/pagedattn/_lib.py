@@ -100,6 +100,8 @@ _SIGNATURES = {
         _c_int,
         [_c_p, _c_p, _c_p, _c_p, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_p, _c_sz, _c_p]),
+    "pagedattn_prefill_plan_device": (
+        _c_int, [_c_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_p, _c_sz]),
     "pagedattn_prefill_run": (
         _c_int,
         [_c_p, _c_p, _c_i64, _c_i64, _c_int, _c_p, _c_p, _c_int, _c_p, _c_int,

@@ -116,9 +116,16 @@ def append_clamp_count() -> int:
     return int(ws[4:8].view(torch.int32)[0].item())
 
 
-def build_batch_indices_positions(append_indptr: torch.Tensor, seq_lens: torch.Tensor) -> None:
-    """(src/models/llama.py:70-83)"""
-    nnz = int(append_indptr[-1].item())
+def build_batch_indices_positions(append_indptr: torch.Tensor, seq_lens: torch.Tensor,
+                                  nnz: int | None = None) -> None:
+    """(src/models/llama.py:70-83).  The token count comes from `nnz` when
+    the caller knows it (the rows of its q, or the token capacity it gave
+    build_paged_metadata, which fills qo_indptr on the device): then nothing
+    is copied to the host.  Otherwise it is read from append_indptr[-1] as
+    the reference does -- without a sync when append_indptr lives on the
+    host, with one device-to-host copy when it lives on the GPU."""
+    if nnz is None:
+        nnz = int(append_indptr[-1].item())
     FlashInferState.batch_indices, FlashInferState.positions = ops.get_batch_indices_positions(
         append_indptr, seq_lens, nnz)
 
@@ -131,15 +138,19 @@ def _q_dtype() -> torch.dtype:
 
 def plan_prefill(*, qo_indptr: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
                  kv_last_page_len: torch.Tensor, num_qo_heads: int, num_kv_heads: int,
-                 head_dim: int) -> None:
-    """(src/models/llama.py:86-116)"""
+                 head_dim: int, max_qo_tokens: int | None = None) -> None:
+    """(src/models/llama.py:86-116).  With max_qo_tokens (a bound on the
+    step's query tokens) the plan is made on the device by every run: the
+    metadata tensors are read in place and nothing is copied to the host, as
+    a step captured in a HIP graph needs."""
     FlashInferState.mode = "prefill"
     FlashInferState.kv_indptr = kv_indptr
     FlashInferState.kv_indices = kv_indices
     FlashInferState.kv_last_page_len = kv_last_page_len
     pw = cast(ops.BatchPrefillWithPagedKVCacheWrapper, FlashInferState.prefill_wrapper)
     pw.begin_forward(qo_indptr, kv_indptr, kv_indices, kv_last_page_len, num_qo_heads,
-                     num_kv_heads, head_dim, FlashInferState.page_size, q_data_type=_q_dtype())
+                     num_kv_heads, head_dim, FlashInferState.page_size, q_data_type=_q_dtype(),
+                     device_plan=max_qo_tokens is not None, max_qo_tokens=max_qo_tokens)
 
 
 def plan_decode(*, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,

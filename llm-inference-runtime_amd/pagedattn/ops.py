@@ -741,7 +741,14 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
 class BatchPrefillWithPagedKVCacheWrapper(_WrapperBase):
     """Ragged-query, paged-KV attention with GQA and a bottom-right aligned
     causal mask (src/models/llama.py:55-60, :86-116, :212-228): row i of
-    sequence b sees kv token j iff j <= kv_len_b - qo_len_b + i."""
+    sequence b sees kv token j iff j <= kv_len_b - qo_len_b + i.
+
+    `plan(..., device_plan=True, max_qo_tokens=n)` reads nothing on the
+    host: every run cuts the q-tiles of the qo_indptr / paged_kv_indptr it
+    was planned with, in their current contents, on the device, for up to n
+    query tokens per run, so a chunked-prefill step can be captured in a HIP
+    graph and replayed while the metadata changes in place.  The outputs are
+    those of a host plan, bit for bit."""
 
     def plan(self, qo_indptr: torch.Tensor, paged_kv_indptr: torch.Tensor,
              paged_kv_indices: torch.Tensor, paged_kv_last_page_len: torch.Tensor,
@@ -751,6 +758,7 @@ class BatchPrefillWithPagedKVCacheWrapper(_WrapperBase):
              window_left: int = -1, logits_soft_cap: float | None = None,
              q_data_type="float16", kv_data_type=None, sm_scale: float | None = None,
              rope_scale=None, rope_theta=None, non_blocking: bool = True,
+             device_plan: bool = False, max_qo_tokens: int | None = None,
              **_unused) -> None:
         _unsupported_options(pos_encoding_mode, window_left, logits_soft_cap, custom_mask,
                              packed_custom_mask)
@@ -758,6 +766,42 @@ class BatchPrefillWithPagedKVCacheWrapper(_WrapperBase):
             raise NotImplementedError("head_dim_vo != head_dim_qk")
         if page_size != PAGE_SIZE:
             raise NotImplementedError(f"page_size {page_size} (only 16 is implemented)")
+        device = self._ws.device
+        if device_plan:
+            for name, t in (("qo_indptr", qo_indptr), ("paged_kv_indptr", paged_kv_indptr),
+                            ("paged_kv_indices", paged_kv_indices),
+                            ("paged_kv_last_page_len", paged_kv_last_page_len)):
+                _require_cuda(t, name)
+                if t.dtype != torch.int32 or not t.is_contiguous():
+                    raise ValueError(f"{name} must be a contiguous int32 device tensor "
+                                     "for a device plan (the runs read it in place)")
+            if max_qo_tokens is None:
+                raise ValueError("device_plan needs max_qo_tokens (query tokens per run)")
+            bsz = paged_kv_last_page_len.numel()
+            if qo_indptr.numel() != bsz + 1 or paged_kv_indptr.numel() != bsz + 1:
+                raise ValueError("qo_indptr and paged_kv_indptr need batch_size + 1 entries")
+            self._q_dtype = _dtype_of(q_data_type)
+            call("pagedattn_prefill_plan_device", self._plan.handle, bsz, int(num_qo_heads),
+                 int(num_kv_heads), int(head_dim_qk), int(page_size), int(max_qo_tokens),
+                 ptr(self._ws), self._ws_bytes)
+            self._qo_rows = None  # known on the device only
+            self._device_plan = True
+        else:
+            self._plan_host(qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
+                            num_qo_heads, num_kv_heads, head_dim_qk, page_size, q_data_type)
+            self._device_plan = False
+        self._qo_indptr = _i32(qo_indptr, device)
+        self._indptr = _i32(paged_kv_indptr, device)
+        self._indices = _i32(paged_kv_indices, device)
+        self._last = _i32(paged_kv_last_page_len, device)
+        self._bsz = paged_kv_last_page_len.numel()
+        self._hq, self._hkv, self._d = int(num_qo_heads), int(num_kv_heads), int(head_dim_qk)
+        self._causal = bool(causal)
+        self._sm_scale = sm_scale
+        self._planned = True
+
+    def _plan_host(self, qo_indptr, paged_kv_indptr, paged_kv_indices, paged_kv_last_page_len,
+                   num_qo_heads, num_kv_heads, head_dim_qk, page_size, q_data_type) -> None:
         device = self._ws.device
         qo_h = _host_i32(qo_indptr)
         indptr_h = _host_i32(paged_kv_indptr)
@@ -773,18 +817,17 @@ class BatchPrefillWithPagedKVCacheWrapper(_WrapperBase):
         call("pagedattn_prefill_plan", self._plan.handle, ptr(qo_h), ptr(indptr_h),
              ptr(last_h), bsz, int(num_qo_heads), int(num_kv_heads), int(head_dim_qk),
              int(page_size), ptr(self._ws), self._ws_bytes, _stream(device))
-        self._qo_indptr = _i32(qo_indptr, device)
         self._qo_rows = int(qo_h[-1]) if bsz else 0
-        self._indptr = _i32(paged_kv_indptr, device)
-        self._indices = _i32(paged_kv_indices, device)
-        self._last = _i32(paged_kv_last_page_len, device)
-        self._bsz, self._hq, self._hkv, self._d = (bsz, int(num_qo_heads), int(num_kv_heads),
-                                                   int(head_dim_qk))
-        self._causal = bool(causal)
-        self._sm_scale = sm_scale
-        self._planned = True
 
     begin_forward = plan
+
+    @property
+    def plan_kind(self) -> str | None:
+        """"host" (q-tile list built by plan()), "device" (built on the
+        device by every run), or None before plan()."""
+        if not self._planned:
+            return None
+        return "device" if self._device_plan else "host"
 
     def run(self, q: torch.Tensor, paged_kv_cache: torch.Tensor, *,
             kv_scales: torch.Tensor | None = None, out: torch.Tensor | None = None,
@@ -794,7 +837,7 @@ class BatchPrefillWithPagedKVCacheWrapper(_WrapperBase):
             raise RuntimeError("plan()/begin_forward() must be called before run()/forward()")
         num_pages, _, _ = _check_pool(paged_kv_cache, self._hkv, self._d, self._kv_layout)
         _check_rows(q, "q", self._hq, self._d)
-        if q.shape[0] < self._qo_rows:
+        if self._qo_rows is not None and q.shape[0] < self._qo_rows:
             raise ValueError(f"q has {q.shape[0]} rows, qo_indptr needs {self._qo_rows}")
         if q.dtype not in (torch.float16, torch.bfloat16):
             raise NotImplementedError(f"q dtype {q.dtype}")
