@@ -31,8 +31,11 @@ struct MergeItem {
 };
 
 // One prefill work item: query tokens [q_lo, q_hi) of sequence b (relative to
-// qo_indptr[b]) for one KV head and all its query heads; kv tokens
-// [kv_lo, kv_hi) of the causal/visible range (split-KV when slot >= 0).
+// qo_indptr[b]) for one KV head and all its query heads.  slot 1 or 2 flags a
+// paired tile (at most half a workgroup's rows), run for both KV heads of
+// each head pair by the pair's even (1) or odd (2) head's workgroup; the
+// planners alternate the two so that paired work lands on both XCDs of a
+// pair.  slot -1: an ordinary tile.
 struct PrefillItem {
   int32_t b, q_lo, q_hi, slot;
 };

@@ -321,14 +321,15 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       p.causal ? min(kv_len, max(0, diag + q_lo + 1)) : kv_len;
   const int n_tiles = (kv_end + BN - 1) / BN;
   // A paired tile (flagged by the planner; at most half the workgroup's rows)
-  // is run for KV heads h and h + 1 by the even-head workgroup: waves
-  // 0 .. WAVES/2 - 1 take head h, the others head h + 1, each group with its
-  // own K/V stages.  Both groups walk the same tiles, so they meet at every
-  // barrier.  The odd-head workgroup has nothing left to do.
-  const bool paired = PAIRS && (p.hkv & 1) == 0 &&
-                      uniform(load_invariant(itp + 3)) == 1 &&
+  // is run for KV heads h0 = h & ~1 and h0 + 1 by one workgroup of the pair,
+  // the even head's (flag 1) or the odd head's (flag 2): waves
+  // 0 .. WAVES/2 - 1 take head h0, the others head h0 + 1, each group with
+  // its own K/V stages.  Both groups walk the same tiles, so they meet at
+  // every barrier.  The pair's other workgroup has nothing left to do.
+  const int pflag = uniform(load_invariant(itp + 3));
+  const bool paired = PAIRS && (p.hkv & 1) == 0 && (pflag == 1 || pflag == 2) &&
                       (q_hi - q_lo) * g <= C::ROWS / 2;
-  if (paired && (h & 1)) return;
+  if (paired && (h & 1) != pflag - 1) return;
 
   // The tile loop of one head group: NW waves, wave index `wave` within the
   // group, KV head `h`, LDS stages st0 / st1.
@@ -600,10 +601,11 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
 
   if constexpr (PAIRS) {
     if (paired) {
+      const int h0 = h & ~1;
       if (wave < C::WAVES / 2)
-        body(std::true_type{}, stage0, stage1, wave, h);
+        body(std::true_type{}, stage0, stage1, wave, h0);
       else
-        body(std::true_type{}, stage2, stage3, wave - C::WAVES / 2, h + 1);
+        body(std::true_type{}, stage2, stage3, wave - C::WAVES / 2, h0 + 1);
       return;
     }
   }
@@ -723,10 +725,17 @@ __global__ void __launch_bounds__(kPrefillPlanThreads) prefill_plan_kernel(Prefi
       const long long mk = key[t];
       int rank = 0;
       for (int j = 0; j < n_tiles; ++j) rank += key[j] > mk ? 1 : 0;
+      // paired tiles alternate between the even and the odd head of a head
+      // pair by list position, so both XCDs of the pair share them
+      if (it.slot > 0) it.slot = 1 + (rank & 1);
       a.items[rank] = it;
     }
   } else {
-    for (int i = t; i < n_tiles; i += kPrefillPlanThreads) a.items[i] = tile(i, nullptr);
+    for (int i = t; i < n_tiles; i += kPrefillPlanThreads) {
+      PrefillItem it = tile(i, nullptr);
+      if (it.slot > 0) it.slot = 1 + (i & 1);
+      a.items[i] = it;
+    }
   }
   for (int i = n_tiles + t; i < a.cap; i += kPrefillPlanThreads)
     a.items[i] = PrefillItem{-1, 0, 0, -1};

@@ -98,7 +98,13 @@ int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
   const size_t host_bytes = sizeof(PrefillItem) * items.size();
   plan->host.assign((host_bytes + 3) / 4, 0);
   auto* dst = reinterpret_cast<PrefillItem*>(plan->host.data());
-  for (size_t i = 0; i < order.size(); ++i) dst[i] = items[order[i]];
+  // paired tiles alternate between the even and the odd head of each pair in
+  // list order, so the two XCDs that hold a head pair's workgroups share them
+  int n_paired = 0;
+  for (size_t i = 0; i < order.size(); ++i) {
+    dst[i] = items[order[i]];
+    if (dst[i].slot > 0) dst[i].slot = 1 + (n_paired++ & 1);
+  }
   plan->workspace = workspace;
   plan->workspace_bytes = workspace_bytes;
   rc = upload_plan(plan, who, host_bytes, ws_align(kWsHeader + host_bytes),
