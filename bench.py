@@ -455,7 +455,19 @@ def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
     graph1_ms = statistics.median(time_steps(lambda i: graphs[i % reps].replay(), steps, warmup))
     # an engine captures a whole forward (every layer's call) in one graph:
     # `steps` calls in one graph spread the graph launch over them
-    graph_ms = _time_graph_ms(lambda i: step(inst[i % reps]), steps, warmup)
+    deal_graph_ms = _time_graph_ms(lambda i: step(inst[i % reps]), steps, warmup)
+    # the engine step as a graph captures it: the step's items dealt once
+    # (update_plan, as plan_decode once per step) and then every layer's run
+    # reading that deal; per-layer time = the step's time / layers
+    layers = 22  # TinyLlama-1.1B decoder layers
+
+    def engine_step(i):
+        dw.update_plan()
+        for layer in range(layers):
+            step(inst[(i * layers + layer) % reps])
+
+    update_ms = _time_graph_ms(lambda i: dw.update_plan(), steps, warmup)
+    graph_ms = _time_graph_ms(engine_step, 3, 1) / layers
     m = w.meta
     npg = np.diff(m.kv_indptr)
     tables = np.full((m.batch_size, int(npg.max())), -1, dtype=np.int32)
@@ -471,9 +483,17 @@ def bench_device_plan(w, dev, dtype, steps: int = 30, warmup: int = 5) -> dict:
     return {"plan_kind": dw.plan_kind,
             "eager_ms_per_step": eager_ms, "eager_GBps": alg_step / (eager_ms * 1e-3) / 1e9,
             "graph_ms_per_step": graph_ms, "graph_GBps": alg_step / (graph_ms * 1e-3) / 1e9,
-            "graph_steps_per_graph": steps,
+            "graph_layers_per_update": layers,
+            "update_plan_ms": update_ms,
+            "dealing_graph_ms_per_step": deal_graph_ms,
+            "dealing_graph_GBps": alg_step / (deal_graph_ms * 1e-3) / 1e9,
+            "dealing_graph_steps_per_graph": steps,
             "graph_one_step_ms": graph1_ms,
-            "metadata_build_ms": meta_ms}
+            "metadata_build_ms": meta_ms,
+            "note": "graph_*: one captured engine step = update_plan (the step's items dealt "
+                    "once on the device) + 22 layer runs reading that deal, per layer; "
+                    "dealing_graph_*: runs that each deal in their prologue, `steps` per graph; "
+                    "eager_*: dealing runs launched one by one"}
 
 
 def bench_kv_write(dev, steps: int = 20, warmup: int = 3) -> dict:

@@ -282,6 +282,25 @@ int pagedattn_decode_plan_device(pagedattn_plan* plan, int32_t batch_size,
                                  int32_t head_dim, int32_t page_size, void* workspace,
                                  size_t workspace_bytes);
 
+/* The device half of BatchDecodeWithPagedKVCacheWrapper.begin_forward
+ * (src/models/llama.py:119-147) for a device shared-item plan: one
+ * one-workgroup launch on `stream` deals the (sequence, KV head) items of
+ * the metadata now in kv_indptr / kv_last_page_len to the workgroups (the
+ * same deal every run of the plan makes in its prologue otherwise) and
+ * writes them, with their page ranges, into the workspace.  Until the next
+ * pagedattn_decode_plan_device, runs of this plan read that table instead
+ * of dealing: the metadata they are given must be the metadata of the last
+ * update, as a FlashInfer run's must be its plan's.  So an engine step calls
+ * it once after writing the step's metadata and then runs every layer; the
+ * launch has a fixed shape and no host synchronisation, so it is captured
+ * in a HIP graph with the runs.  Outputs are bit-identical to runs that deal
+ * on their own.  For a device split plan (pagedattn_decode_plan_kind
+ * PAGEDATTN_DECODE_DEVICE) there is nothing to deal ahead and the call
+ * returns PAGEDATTN_OK without a launch.  The table takes CUs x 8 x 32
+ * bytes after the 256-byte workspace header. */
+int pagedattn_decode_plan_device_update(pagedattn_plan* plan, const int32_t* kv_indptr,
+                                        const int32_t* kv_last_page_len, void* stream);
+
 /* Which partition a decode plan holds (a diagnostic with no counterpart in
  * the reference, for tests and benchmarks): PAGEDATTN_DECODE_SPLIT (a work
  * list of head groups; sequences cut between groups are merged by a second

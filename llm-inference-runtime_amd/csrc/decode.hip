@@ -874,6 +874,82 @@ __device__ __forceinline__ int dev_item_table(const DecodeParams& p, SharedLds<D
   return n_it;
 }
 
+// The same deal as dev_item_table, made once for all the runs that share
+// the metadata (pagedattn_decode_plan_device_update): one workgroup ranks the
+// sequences and writes every workgroup's items, page ranges and chunk offsets
+// in the host plan's layout, so the attention launches read their items as a
+// host-planned shared run does (no ranking in their prologue).  Threads are
+// sequences for the ranking and workgroups for the table.
+struct SharedTableArgs {
+  const int32_t* kv_indptr;
+  const int32_t* last_page_len;
+  int32_t batch_size, hkv, n_wg;
+  SharedItem* items;  // n_wg * kSharedMaxItems entries
+  int32_t* fault_count;
+};
+
+constexpr int kSharedTableThreads = 1024;
+
+__global__ void __launch_bounds__(kSharedTableThreads) decode_shared_table_kernel(SharedTableArgs a) {
+  static_assert(kDevSharedMaxBatch <= kSharedTableThreads, "one sequence per thread");
+  __shared__ int ip[kDevSharedMaxBatch + 1];
+  __shared__ int lastp[kDevSharedMaxBatch];
+  __shared__ __attribute__((aligned(16))) int key[kDevSharedMaxBatch];
+  __shared__ int order[kDevSharedMaxBatch];  // sequence of each rank
+  const int t = (int)threadIdx.x;
+  const int B = a.batch_size, H = a.hkv, nwg = a.n_wg;
+  const int N = B * H;
+  if (B <= 0 || B > kDevSharedMaxBatch || H <= 0 || N > kSharedMaxItems * nwg) {
+    // a plan the entry point would not make: every workgroup gets no items
+    for (int i = t; i < nwg * kSharedMaxItems; i += kSharedTableThreads)
+      a.items[i] = SharedItem{-1, 0, 0, 0, -1, 0, kPage, 0};
+    if (t == 0) count_lanes(a.fault_count, true);
+    return;
+  }
+  for (int i = t; i <= B; i += kSharedTableThreads) {
+    ip[i] = a.kv_indptr[i];
+    if (i < B) lastp[i] = a.last_page_len[i];
+  }
+  __syncthreads();
+  // keys and ranks as dev_item_table: more pages first, then smaller index
+  constexpr int kKeyIdx = 1024;  // > kDevSharedMaxBatch
+  const int B16 = (B + 15) & ~15;
+  if (t < B16)
+    key[t] = t < B ? min(max(0, ip[t + 1] - ip[t]), (1 << 21) - 1) * kKeyIdx + (kKeyIdx - 1 - t)
+                   : -1;
+  __syncthreads();
+  if (t < B) {
+    const int kb = key[t];
+    int rank = 0;
+    for (int j = 0; j < B16; j += 4) {
+      const int4 v = *reinterpret_cast<const int4*>(key + j);
+      rank += (v.x > kb) + (v.y > kb) + (v.z > kb) + (v.w > kb);
+    }
+    order[rank] = t;
+  }
+  __syncthreads();
+  // workgroup w's round-r item is item r nwg + w (r even) or
+  // r nwg + nwg - 1 - w (r odd) of the rank order, heads in order
+  for (int w = t; w < nwg; w += kSharedTableThreads) {
+    int n_it = 0;
+    for (int r = 0; r < kSharedMaxItems; ++r)
+      if (r * nwg + ((r & 1) ? nwg - 1 - w : w) < N) n_it = r + 1;
+    int acc = 0;
+    for (int r = 0; r < kSharedMaxItems; ++r) {
+      SharedItem it{-1, 0, 0, 0, -1, 0, kPage, n_it};
+      if (r < n_it) {
+        const int i = r * nwg + ((r & 1) ? nwg - 1 - w : w);
+        const int b = order[i / H];
+        const int np = max(0, ip[b + 1] - ip[b]);
+        const int nc = max(1, (np + 2 * kSharedStagePairs - 1) / (2 * kSharedStagePairs));
+        it = SharedItem{b, i - (i / H) * H, acc, nc, ip[b], np, lastp[b], n_it};
+        acc += nc;
+      }
+      a.items[(int64_t)w * kSharedMaxItems + r] = it;
+    }
+  }
+}
+
 template <int D, bool BF16, bool FP8, bool APPEND, bool ROPE, bool DEV>
 __global__ void __launch_bounds__(256, 1) decode_shared_kernel(DecodeParams p) {
   using Tr = DecodeTraits<D, BF16, FP8>;
@@ -1485,9 +1561,11 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
   hipStream_t s = (hipStream_t)stream;
   const bool bf16 = q_dtype == PAGEDATTN_BF16;
   if (plan->shared) {
-    // a device-planned shared plan (implicit) finds its items from kv_indptr
+    // a device-planned shared plan (implicit) finds its items from kv_indptr,
+    // unless pagedattn_decode_plan_device_update has dealt them into the
+    // workspace (read as a host plan's)
     DecodeFn fn = pick_decode_shared(plan->d, bf16, fp8, app != nullptr, app && app->rope,
-                                     plan->implicit);
+                                     plan->implicit && !plan->dev_table);
     if (!fn)
       return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: shared-item plan for D = %d", who,
                        plan->d);
@@ -1528,6 +1606,31 @@ static int decode_run_impl(const char* who, const pagedattn_plan* plan,
 }  // namespace pa
 
 extern "C" {
+
+int pagedattn_decode_plan_device_update(pagedattn_plan* plan, const int32_t* kv_indptr,
+                                        const int32_t* kv_last_page_len, void* stream) {
+  const char* who = "decode_plan_device_update";
+  if (!plan || plan->mode != kPlanDecode || !plan->implicit)
+    return set_error(PAGEDATTN_ERR_PLAN, "%s: no device decode plan (call plan_device first)",
+                     who);
+  if (!plan->shared) return PAGEDATTN_OK;  // the split partition is made by every run
+  if (!kv_indptr || !kv_last_page_len)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: null pointer", who);
+  const size_t bytes = sizeof(SharedItem) * (size_t)plan->n_items * kSharedMaxItems;
+  if (!plan->workspace || plan->workspace_bytes < kWsHeader + bytes)
+    return set_error(PAGEDATTN_ERR_WORKSPACE, "%s: the item table needs %zu bytes after the "
+                     "workspace header", who, bytes);
+  SharedTableArgs a{kv_indptr, kv_last_page_len, plan->batch_size, plan->hkv, plan->n_items,
+                    reinterpret_cast<SharedItem*>(static_cast<char*>(plan->workspace) + kWsHeader),
+                    static_cast<int32_t*>(plan->workspace) + 2};
+  hipLaunchKernelGGL(decode_shared_table_kernel, dim3(1), dim3(kSharedTableThreads), 0,
+                     (hipStream_t)stream, a);
+  const int rc = check_launch(who);
+  if (rc) return rc;
+  plan->items_dev = a.items;
+  plan->dev_table = true;
+  return PAGEDATTN_OK;
+}
 
 int pagedattn_decode_run(const pagedattn_plan* plan, const void* q,
                          int64_t q_stride_n, int64_t q_stride_h,

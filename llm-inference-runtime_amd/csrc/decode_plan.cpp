@@ -265,6 +265,7 @@ int setup_device_plan(const char* who, pagedattn_plan* plan, int32_t batch_size,
                      "available", who, end, bytes);
   plan->implicit = true;
   plan->shared = false;
+  plan->dev_table = false;
   plan->item_cost = decode_item_cost();
   plan->batch_size = batch_size;
   plan->hq = num_qo_heads;
@@ -328,6 +329,7 @@ int pagedattn_decode_plan(pagedattn_plan* plan, const int32_t* kv_indptr_host,
   int cus = device_cu_count();
   if (cus <= 0) cus = 256;
   plan->shared = false;
+  plan->dev_table = false;
 
   if (split_pages == 0 && decode_shared_mode() != 0) {
     std::vector<SharedItem> sitems;

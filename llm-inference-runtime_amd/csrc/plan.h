@@ -104,6 +104,10 @@ struct pagedattn_plan {
   bool shared = false;
   // decode, shared: fixed chunk assignment (output bits independent of timing)
   bool deterministic = false;
+  // decode, implicit and shared: the items were dealt into the workspace by
+  // pagedattn_decode_plan_device_update (items_dev, the host plan's layout)
+  // and the runs read them there instead of dealing in their prologue
+  bool dev_table = false;
   // prefill: query tokens per tile (rows = tokens * hq/hkv)
   int q_tile = 0;
   // prefill: tiles of at most half a workgroup's rows run as KV-head pairs

@@ -649,6 +649,23 @@ class BatchDecodeWithPagedKVCacheWrapper(_WrapperBase):
 
     begin_forward = plan
 
+    def update_plan(self) -> None:
+        """For a device plan: deal the (sequence, KV head) items of the
+        metadata now in the plan's indptr / last_page_len tensors to the
+        workgroups, on the device and the current stream (one small launch,
+        no host synchronisation, captured with the runs in a HIP graph).
+        Until the next plan(), every run reads that deal instead of making
+        its own in its prologue, so the metadata must not change between
+        this call and the runs it serves: an engine step calls it once after
+        writing the step's metadata, before the layers' runs.  A no-op for
+        host plans and for device plans of the split kind."""
+        if not self._planned:
+            raise RuntimeError("plan() must be called before update_plan()")
+        if self.plan_kind != "device_shared":
+            return
+        call("pagedattn_decode_plan_device_update", self._plan.handle, ptr(self._indptr),
+             ptr(self._last), _stream(self._indptr.device))
+
     @property
     def plan_kind(self) -> str | None:
         """The partition the current plan holds: "split" (head-group work

@@ -225,7 +225,8 @@ class _Step:
     and lengths, then RoPE + append + attention (+ merge) in the fused
     launch."""
 
-    def __init__(self, gpu, tables, maxp, hq, hkv, d, graph):
+    def __init__(self, gpu, tables, maxp, hq, hkv, d, graph, table=False):
+        self.table = table  # deal the items once per step (update_plan) for the runs
         self.bsz = len(tables)
         self.bt = _tables_tensor(tables, maxp, gpu)
         self.lens = torch.zeros(self.bsz, dtype=torch.int32, device=gpu)
@@ -245,16 +246,24 @@ class _Step:
 
     def __call__(self, pool):
         pagedattn.build_paged_metadata(self.bt, self.lens, out=self.buf)
+        if self.table:
+            self.w.update_plan()
         self.w.run(self.q, pool, out=self.out, append_key=self.k, append_value=self.v,
                    rope=(1.0, 5e5), positions=self.buf.positions)
 
 
-@pytest.mark.parametrize("bsz,hq,hkv,d,kind", [
-    (48, 32, 8, 128, "device"),           # 384 items: the split device partition
-    (128, 32, 8, 128, "device_shared"),   # 1024 items: whole items dealt on the device
-    (256, 32, 4, 64, "device_shared"),    # the TinyLlama batch shape
+@pytest.mark.parametrize("bsz,hq,hkv,d,kind,table", [
+    (48, 32, 8, 128, "device", False),           # 384 items: the split device partition
+    (48, 32, 8, 128, "device", True),            # (update_plan is a no-op there)
+    (128, 32, 8, 128, "device_shared", False),   # 1024 items: whole items dealt on the device
+    (256, 32, 4, 64, "device_shared", False),    # the TinyLlama batch shape
+    (128, 32, 8, 128, "device_shared", True),    # dealt once per step by update_plan
+    (256, 32, 4, 64, "device_shared", True),
 ])
-def test_decode_step_graph_replay(gpu, bsz, hq, hkv, d, kind):
+def test_decode_step_graph_replay(gpu, bsz, hq, hkv, d, kind, table):
+    """The graphed step (with `table`: metadata, update_plan and the run
+    captured together) equals the eager step that deals in every run, bit
+    for bit, every replay."""
     rng = np.random.default_rng(11)
     start = [int(x) for x in rng.integers(1, 3000, bsz)]
     start[0], start[1] = 15, 16  # crosses a page boundary in the first replays
@@ -266,7 +275,7 @@ def test_decode_step_graph_replay(gpu, bsz, hq, hkv, d, kind):
     pool_g = torch.randn((num_pages, 2, hkv, 16, d), generator=g, device=gpu).to(torch.bfloat16)
     pool_e = pool_g.clone()
     eager = _Step(gpu, tables, maxp, hq, hkv, d, graph=False)
-    graphed = _Step(gpu, tables, maxp, hq, hkv, d, graph=True)
+    graphed = _Step(gpu, tables, maxp, hq, hkv, d, graph=True, table=table)
     assert eager.w.plan_kind == graphed.w.plan_kind == kind
     lens0 = torch.tensor(start, dtype=torch.int32, device=gpu)
     graphed.lens.copy_(lens0)
@@ -349,3 +358,56 @@ def test_device_shared_plan(gpu, name, lens, hq, hkv, d, fp8):
     for b in range(len(lens)):
         if lens[b] == 0:
             assert torch.all(out[b] == 0) and torch.all(torch.isinf(lse[b]))
+
+
+@pytest.mark.parametrize("name,lens,hq,hkv,d,fp8", [
+    ("tinyllama", list(np.random.default_rng(21).integers(1, 2049, 300)), 32, 4, 64, False),
+    ("empties", [0, 0, 3] + list(np.random.default_rng(22).integers(1, 700, 260)) + [0],
+     32, 4, 64, False),
+    ("e4m3_d128", list(np.random.default_rng(24).integers(1, 8193, 128)), 64, 8, 128, True),
+    ("max_batch", list(np.random.default_rng(26).integers(1, 400, 512)), 32, 4, 64, False),
+])
+def test_device_shared_table_equals_dealing(gpu, name, lens, hq, hkv, d, fp8):
+    """update_plan deals the items once into the workspace; the runs that
+    read that table give the bits of runs that deal in their prologue, and
+    the table follows the metadata of each update."""
+    lens = [int(x) for x in lens]
+    meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=len(lens) + 5)
+    scales = None
+    if fp8:
+        pool, scales = pagedattn.quantize_pages_e4m3(pool)
+    ws = workspace(gpu)
+    w = pagedattn.BatchDecodeWithPagedKVCacheWrapper(ws, "HND")
+    indptr, last = i32(meta.kv_indptr, gpu), i32(meta.kv_last_page_len, gpu)
+    w.plan(indptr, i32(meta.kv_indices, gpu), last, hq, hkv, d, 16, q_data_type=q.dtype,
+           device_plan=True)
+    assert w.plan_kind == "device_shared"
+    want, want_lse = w.run(q, pool, kv_scales=scales, return_lse=True)
+    w.update_plan()
+    got, got_lse = w.run(q, pool, kv_scales=scales, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(got_lse, want_lse)
+    assert int(ws[8:12].view(torch.int32).item()) == 0
+    # the same plan on other metadata of the batch: a fresh deal per update,
+    # and the new plan() drops the table (runs deal on their own again)
+    lens2 = [max(0, n - 17) for n in lens]
+    meta2, pool2, q2 = decode_case(gpu, lens2, hq, hkv, d, seed=len(lens) + 6)
+    if fp8:
+        pool2, scales = pagedattn.quantize_pages_e4m3(pool2)
+    indptr.copy_(i32(meta2.kv_indptr, gpu))
+    last.copy_(i32(meta2.kv_last_page_len, gpu))
+    ind2 = i32(meta2.kv_indices, gpu)
+    w2 = pagedattn.BatchDecodeWithPagedKVCacheWrapper(workspace(gpu), "HND")
+    w2.plan(indptr, ind2, last, hq, hkv, d, 16, q_data_type=q.dtype, device_plan=True)
+    want2, want2_lse = w2.run(q2, pool2, kv_scales=scales, return_lse=True)
+    w.plan(indptr, ind2, last, hq, hkv, d, 16, q_data_type=q.dtype, device_plan=True)
+    w.update_plan()
+    got2, got2_lse = w.run(q2, pool2, kv_scales=scales, return_lse=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got2, want2) and torch.equal(got2_lse, want2_lse)
+    rows = sorted({0, len(lens2) - 1, int(np.argmax(lens2))} |
+                  set(range(1, len(lens2), max(1, len(lens2) // 10))))
+    rows = [b for b in rows if lens2[b] > 0]
+    ref, ref_lse = oracle_decode(meta2, pool2, q2, batch=rows, scales=scales)
+    tol = 3e-2 if fp8 else 2e-2
+    assert max_err(got2, ref, rows) < tol
