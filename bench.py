@@ -347,6 +347,16 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
 
     dev_ms = _stats(time_steps(attn_dev, args.steps, args.warmup))["ms_median"]
     dev_graph_ms = _time_graph_ms(attn_dev, args.steps, args.warmup)
+    # a captured engine step: the list cut once for the step (update_plan,
+    # as plan_prefill once per step) and every layer's run reading it
+    layers = 32  # Llama-3-8B decoder layers
+
+    def engine_step(i):
+        pd.update_plan()
+        for layer in range(layers):
+            attn_dev(i * layers + layer)
+
+    step_graph_ms = _time_graph_ms(engine_step, 2, 1) / layers
     dropped = int(ws_dev[12:16].view(torch.int32).item())
     res = {
         "workload": label,
@@ -361,7 +371,14 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
                         "attn_TFLOPs": flops / (dev_ms * 1e-3) / 1e12,
                         "graph_ms_per_run": round(dev_graph_ms, 5),
                         "graph_TFLOPs": flops / (dev_graph_ms * 1e-3) / 1e12,
-                        "dropped_tiles": dropped},
+                        "step_graph_ms_per_run": round(step_graph_ms, 5),
+                        "step_graph_TFLOPs": flops / (step_graph_ms * 1e-3) / 1e12,
+                        "step_graph_layers_per_update": layers,
+                        "dropped_tiles": dropped,
+                        "note": "attn_*: runs that each cut their q-tile list (a plan launch "
+                                "ahead of each); graph_*: such runs, `steps` per graph; "
+                                "step_graph_*: one captured engine step = update_plan + 32 "
+                                "runs reading its list, per run"},
     }
     res["frac"] = res["attn_TFLOPs"] / BF16_PEAK_TFLOPS
     res["roofline"] = roofline("mfma", kernel, res["attn_TFLOPs"], flops, ms, label)

@@ -420,6 +420,20 @@ int pagedattn_prefill_plan_device(pagedattn_plan* plan, int32_t batch_size,
                                   int32_t head_dim, int32_t page_size, int64_t max_qo_tokens,
                                   void* workspace, size_t workspace_bytes);
 
+/* The device half of BatchPrefillWithPagedKVCacheWrapper.begin_forward
+ * (src/models/llama.py:86-116) for a device prefill plan: the one-workgroup
+ * launch that cuts the q-tile list from the metadata now in qo_indptr /
+ * kv_indptr / kv_last_page_len, on `stream`, once.  Until the next
+ * pagedattn_prefill_plan_device, runs of this plan launch no list of their
+ * own and read this one: their metadata must be the metadata of the last
+ * update (as a FlashInfer run's must be its plan's), so an engine step calls
+ * it once after writing the step's metadata and then runs every layer.
+ * Fixed shape, no host synchronisation: captured in a HIP graph with the
+ * runs.  Outputs are bit-identical to runs that cut their own list. */
+int pagedattn_prefill_plan_device_update(pagedattn_plan* plan, const int32_t* qo_indptr,
+                                         const int32_t* kv_indptr,
+                                         const int32_t* kv_last_page_len, void* stream);
+
 /* BatchPrefillWithPagedKVCacheWrapper.forward(q, paged_kv_cache, causal)
  * (src/models/llama.py:212-228).  Ragged q [nnz, num_qo_heads, head_dim];
  * with causal != 0, row i of sequence b sees kv token j iff

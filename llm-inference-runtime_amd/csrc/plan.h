@@ -106,7 +106,9 @@ struct pagedattn_plan {
   bool deterministic = false;
   // decode, implicit and shared: the items were dealt into the workspace by
   // pagedattn_decode_plan_device_update (items_dev, the host plan's layout)
-  // and the runs read them there instead of dealing in their prologue
+  // and the runs read them there instead of dealing in their prologue.
+  // prefill, implicit: pagedattn_prefill_plan_device_update built the q-tile
+  // list and the runs launch no plan kernel of their own
   bool dev_table = false;
   // prefill: query tokens per tile (rows = tokens * hq/hkv)
   int q_tile = 0;

@@ -743,9 +743,49 @@ __global__ void __launch_bounds__(kPrefillPlanThreads) prefill_plan_kernel(Prefi
 
 }  // namespace pa
 
+namespace pa {
+
+// The q-tile list of a device prefill plan, cut from the metadata on the
+// device by one workgroup (prefill_plan_kernel) on `stream`.
+static int launch_prefill_plan(const pagedattn_plan* plan, const int32_t* qo_indptr,
+                               const int32_t* kv_indptr, const int32_t* kv_last_page_len,
+                               void* stream, const char* who) {
+  PrefillPlanArgs a{qo_indptr, kv_indptr, kv_last_page_len, plan->batch_size,
+                    plan->q_tile, plan->hq / plan->hkv, plan->prefill_pair ? 1 : 0,
+                    plan->n_items, static_cast<PrefillItem*>(plan->items_dev),
+                    reinterpret_cast<int32_t*>(static_cast<char*>(plan->workspace) + 12)};
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPrefillPlanThreads), 0,
+                     (hipStream_t)stream, a);
+  return check_launch(who);
+}
+
+}  // namespace pa
+
 using namespace pa;
 
 extern "C" {
+
+int pagedattn_prefill_plan_device_update(pagedattn_plan* plan, const int32_t* qo_indptr,
+                                         const int32_t* kv_indptr,
+                                         const int32_t* kv_last_page_len, void* stream) {
+  const char* who = "prefill_plan_device_update";
+  if (!plan || plan->mode != kPlanPrefill || !plan->implicit)
+    return set_error(PAGEDATTN_ERR_PLAN, "%s: no device prefill plan (call plan_device first)",
+                     who);
+  if (!qo_indptr || !kv_indptr || !kv_last_page_len)
+    return set_error(PAGEDATTN_ERR_INVALID, "%s: null pointer", who);
+  if (plan->batch_size > kPrefillDevMaxBatch)
+    return set_error(PAGEDATTN_ERR_UNSUPPORTED, "%s: device plan of %d sequences", who,
+                     plan->batch_size);
+  if (plan->n_items == 0) {
+    plan->dev_table = true;
+    return PAGEDATTN_OK;
+  }
+  const int rc = launch_prefill_plan(plan, qo_indptr, kv_indptr, kv_last_page_len, stream, who);
+  if (rc) return rc;
+  plan->dev_table = true;
+  return PAGEDATTN_OK;
+}
 
 int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
                           int64_t q_stride_n, int64_t q_stride_h,
@@ -815,15 +855,10 @@ int pagedattn_prefill_run(const pagedattn_plan* plan, const void* q,
   p.causal = causal ? 1 : 0;
   p.scale_log2 = sm_scale * 1.4426950408889634f;
   PrefillFn fn = pick_prefill(plan->d, q_dtype == PAGEDATTN_BF16, fp8);
-  if (plan->implicit) {
+  if (plan->implicit && !plan->dev_table) {
     // the work list of this run, built on the device ahead of the attention
-    PrefillPlanArgs a{qo_indptr, kv_indptr, kv_last_page_len, plan->batch_size,
-                      plan->q_tile, p.g, plan->prefill_pair ? 1 : 0, plan->n_items,
-                      static_cast<PrefillItem*>(plan->items_dev),
-                      reinterpret_cast<int32_t*>(static_cast<char*>(plan->workspace) + 12)};
-    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPrefillPlanThreads), 0,
-                       (hipStream_t)stream, a);
-    int rc = check_launch(who);
+    // (unless pagedattn_prefill_plan_device_update built it for the step)
+    int rc = launch_prefill_plan(plan, qo_indptr, kv_indptr, kv_last_page_len, stream, who);
     if (rc) return rc;
   }
   hipLaunchKernelGGL(fn, dim3(plan->n_items * plan->hkv), dim3(64 * kPrefillWaves), 0,

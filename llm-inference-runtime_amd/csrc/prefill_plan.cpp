@@ -124,6 +124,7 @@ int pagedattn_prefill_plan(pagedattn_plan* plan, const int32_t* qo_indptr_host,
   plan->items_dev = static_cast<char*>(workspace) + kWsHeader;
   plan->implicit = false;
   plan->shared = false;
+  plan->dev_table = false;
   plan->mode = kPlanPrefill;
   return PAGEDATTN_OK;
 }
@@ -160,6 +161,7 @@ int pagedattn_prefill_plan_device(pagedattn_plan* plan, int32_t batch_size,
   plan->workspace_bytes = workspace_bytes;
   plan->implicit = true;
   plan->shared = false;
+  plan->dev_table = false;
   plan->prefill_pair = prefill_pairing() && num_kv_heads % 2 == 0;
   plan->batch_size = batch_size;
   plan->hq = num_qo_heads;

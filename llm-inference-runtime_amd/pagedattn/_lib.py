@@ -92,6 +92,7 @@ _SIGNATURES = {
     "pagedattn_decode_plan_device": (
         _c_int, [_c_p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_p, _c_sz]),
     "pagedattn_decode_plan_device_update": (_c_int, [_c_p, _c_p, _c_p, _c_p]),
+    "pagedattn_prefill_plan_device_update": (_c_int, [_c_p, _c_p, _c_p, _c_p, _c_p]),
     "pagedattn_decode_plan_kind": (_c_int, [_c_p]),
     "pagedattn_build_paged_metadata": (
         _c_int,

@@ -838,10 +838,27 @@ class BatchPrefillWithPagedKVCacheWrapper(_WrapperBase):
 
     begin_forward = plan
 
+    def update_plan(self) -> None:
+        """For a device plan: cut the q-tile list of the metadata now in the
+        plan's qo_indptr / paged_kv_indptr / paged_kv_last_page_len tensors,
+        on the device and the current stream (one small launch, captured
+        with the runs in a HIP graph).  Until the next plan(), the runs read
+        that list instead of cutting their own, so the metadata must not
+        change between this call and the runs it serves: an engine step
+        calls it once after writing the step's metadata, before the layers'
+        runs.  A no-op for host plans."""
+        if not self._planned:
+            raise RuntimeError("plan() must be called before update_plan()")
+        if not self._device_plan:
+            return
+        call("pagedattn_prefill_plan_device_update", self._plan.handle, ptr(self._qo_indptr),
+             ptr(self._indptr), ptr(self._last), _stream(self._qo_indptr.device))
+
     @property
     def plan_kind(self) -> str | None:
         """"host" (q-tile list built by plan()), "device" (built on the
-        device by every run), or None before plan()."""
+        device by every run, or once per update_plan()), or None before
+        plan()."""
         if not self._planned:
             return None
         return "device" if self._device_plan else "host"

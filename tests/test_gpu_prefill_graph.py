@@ -37,7 +37,7 @@ def _dropped(ws):
 
 
 def _prefill(gpu, meta, pool, q, hq, hkv, d, *, device_plan, causal=True, scales=None,
-             ws=None, max_qo_tokens=None, out=None):
+             ws=None, max_qo_tokens=None, out=None, update=False):
     ws = workspace(gpu) if ws is None else ws
     w = pagedattn.BatchPrefillWithPagedKVCacheWrapper(ws, "HND")
     kw = {}
@@ -47,6 +47,8 @@ def _prefill(gpu, meta, pool, q, hq, hkv, d, *, device_plan, causal=True, scales
     w.plan(i32(meta.qo_indptr, gpu), i32(meta.kv_indptr, gpu), i32(meta.kv_indices, gpu),
            i32(meta.kv_last_page_len, gpu), hq, hkv, d, 16, q_data_type=q.dtype, **kw)
     assert w.plan_kind == ("device" if device_plan else "host")
+    if update:
+        w.update_plan()  # the q-tile list cut once; the run launches none
     if out is None:
         out = torch.full((q.shape[0], hq, d), float("nan"), dtype=q.dtype, device=gpu)
     lse = torch.full((q.shape[0], hq), float("nan"), device=gpu)
@@ -89,6 +91,11 @@ def test_prefill_device_plan_equals_host_plan(gpu, name, causal):
     o_d2, l_d2, _ = _prefill(gpu, meta, pool, q, hq, hkv, d, device_plan=True, causal=causal,
                              scales=scales, ws=ws)
     assert torch.equal(o_d2, o_h) and torch.equal(l_d2, l_h)
+    # and a run that reads the list update_plan cut ahead of it
+    o_u, l_u, ws_u = _prefill(gpu, meta, pool, q, hq, hkv, d, device_plan=True, causal=causal,
+                              scales=scales, update=True)
+    assert torch.equal(o_u, o_h) and torch.equal(l_u, l_h)
+    assert _dropped(ws_u) == 0
     if name in ("edges_d64", "e4m3_70b"):
         # and the oracle, on some rows (the bit equality covers the rest)
         b = len(meta.kv_last_page_len) - 1 if name == "edges_d64" else 0
@@ -156,7 +163,8 @@ class _PrefillStep:
     new K rows with the page append (one launch), then prefill attention with
     a device plan.  Nothing is read on the host."""
 
-    def __init__(self, gpu, tables, maxp, tokens, hq, hkv, d):
+    def __init__(self, gpu, tables, maxp, tokens, hq, hkv, d, table=False):
+        self.table = table  # the q-tile list cut once per step (update_plan) for the run
         bsz = len(tables)
         self.bt = _tables_tensor(tables, maxp, gpu)
         self.lens = torch.zeros(bsz, dtype=torch.int32, device=gpu)
@@ -178,10 +186,15 @@ class _PrefillStep:
                                        self.buf.positions, pool, self.buf.kv_indices,
                                        self.buf.kv_indptr, self.buf.kv_last_page_len,
                                        kv_layout="HND", rope_scale=1.0, rope_theta=5e5)
+        if self.table:
+            self.w.update_plan()
         self.w.run(self.q, pool, out=self.out, lse=self.lse)
 
 
-def test_chunked_prefill_step_graph_replay(gpu):
+@pytest.mark.parametrize("table", [False, True])
+def test_chunked_prefill_step_graph_replay(gpu, table):
+    """The graphed step (with `table`: its q-tile list cut by update_plan
+    inside the graph) equals the eager step whose run cuts its own list."""
     hq, hkv, d = 32, 8, 128
     rng = np.random.default_rng(31)
     bsz = 8
@@ -198,7 +211,7 @@ def test_chunked_prefill_step_graph_replay(gpu):
     pool_g = torch.randn((num_pages, 2, hkv, 16, d), generator=g, device=gpu).to(torch.bfloat16)
     pool_e = pool_g.clone()
     eager = _PrefillStep(gpu, tables, maxp, tokens, hq, hkv, d)
-    graphed = _PrefillStep(gpu, tables, maxp, tokens, hq, hkv, d)
+    graphed = _PrefillStep(gpu, tables, maxp, tokens, hq, hkv, d, table=table)
     lens = torch.tensor(start, dtype=torch.int32, device=gpu)
     first = torch.tensor(plans[0], dtype=torch.int32, device=gpu)
     graphed.lens.copy_(lens + first)
