@@ -805,10 +805,23 @@ struct ChunkRef {
 // involved.
 // Fills L.b / h / chunk_lo / n_chunks of the workgroup's items; returns
 // their number (uniform).
+// The workgroups of the device deal are relabelled: workgroup w takes the
+// items the alternating deal gives to position deal_pos(w), whose inverse
+// sends each aligned group of 8 positions (the KV heads of a sequence, whose
+// pages share a scale block) to workgroups of one XCD (workgroup w runs on
+// XCD w mod 8).  Every workgroup's item list is one of the plain deal's, so
+// the balance and the output bits are those of the plain deal.
+__device__ __forceinline__ int deal_pos(int w, int nwg) {
+  if (nwg % 8) return w;
+  const int m = nwg / 8;
+  return (w % m) * 8 + w / m;
+}
+
 template <int D>
 __device__ __forceinline__ int dev_item_table(const DecodeParams& p, SharedLds<D>& L, int* ip,
                                               int* lastp, int* key) {
-  const int B = p.batch_size, H = p.hkv, nwg = (int)gridDim.x, w = (int)blockIdx.x;
+  const int B = p.batch_size, H = p.hkv, nwg = (int)gridDim.x;
+  const int w = deal_pos((int)blockIdx.x, nwg);
   const int N = B * H;
   if (B <= 0 || B > kDevSharedMaxBatch || N > kSharedMaxItems * nwg) {
     // a launch the plan did not make (the host plan keeps both bounds)
@@ -928,9 +941,11 @@ __global__ void __launch_bounds__(kSharedTableThreads) decode_shared_table_kerne
     order[rank] = t;
   }
   __syncthreads();
-  // workgroup w's round-r item is item r nwg + w (r even) or
-  // r nwg + nwg - 1 - w (r odd) of the rank order, heads in order
-  for (int w = t; w < nwg; w += kSharedTableThreads) {
+  // workgroup wg's round-r item is item r nwg + w (r even) or
+  // r nwg + nwg - 1 - w (r odd) of the rank order, heads in order, with
+  // w = deal_pos(wg) as in the prologue's deal
+  for (int wg = t; wg < nwg; wg += kSharedTableThreads) {
+    const int w = deal_pos(wg, nwg);
     int n_it = 0;
     for (int r = 0; r < kSharedMaxItems; ++r)
       if (r * nwg + ((r & 1) ? nwg - 1 - w : w) < N) n_it = r + 1;
@@ -945,7 +960,7 @@ __global__ void __launch_bounds__(kSharedTableThreads) decode_shared_table_kerne
         it = SharedItem{b, i - (i / H) * H, acc, nc, ip[b], np, lastp[b], n_it};
         acc += nc;
       }
-      a.items[(int64_t)w * kSharedMaxItems + r] = it;
+      a.items[(int64_t)wg * kSharedMaxItems + r] = it;
     }
   }
 }
