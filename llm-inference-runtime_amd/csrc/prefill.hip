@@ -426,6 +426,13 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       pid = pid_next;
       pid_next = fetch_page_ids(p, ind_lo, npages, t + 2, lane);
       const int pid_ld = t + 1 < n_tiles ? pid : -1;  // past the last tile: no pages
+      if constexpr (!FP8) {
+        // tile t + 1 straight into the other stage, K and V, a whole tile
+        // ahead of the barrier that waits for it
+        dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid_ld, npages, last, t + 1, nxt, wave, lane);
+        dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid_ld, npages, last, t + 1, nxt + C::TILEB,
+                                             wave, lane);
+      }
 
       // ---- S^T = K . Q^T
       f32x16 s[RB][2];
@@ -441,12 +448,8 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
           for (int rb = 0; rb < RB; ++rb) s[rb][mt] = mfma32<BF16>(a, qf[rb][ks_], s[rb][mt]);
         }
         if (mt == 0) {
-          if constexpr (FP8) {
+          if constexpr (FP8)
             load_half<D, BF16, FP8, RB, false>(kr, p, h, pid_ld, npages, last, t + 1, wave, lane);
-          } else {
-            dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid_ld, npages, last, t + 1, nxt, wave,
-                                                  lane);
-          }
         }
       }
 
@@ -517,12 +520,8 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         if (st == 1) {
-          if constexpr (FP8) {
+          if constexpr (FP8)
             load_half<D, BF16, FP8, RB, true>(vr, p, h, pid_ld, npages, last, t + 1, wave, lane);
-          } else {
-            dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid_ld, npages, last, t + 1,
-                                                 nxt + C::TILEB, wave, lane);
-          }
         }
         u32x4 pb[RB];
 #pragma unroll
