@@ -213,16 +213,33 @@ __device__ __forceinline__ void rope8(u32x4& lo, u32x4& hi, const float (&c)[8],
 }
 
 // wave-level reductions over lanes that differ in bits 4 and 5 (the four
-// 16-lane groups of a 16x16 MFMA tile).
+// 16-lane groups of a 16x16 MFMA tile).  v_permlane16_swap / 32_swap
+// exchange 16-lane rows (lanes l and l ^ 16) and the two 32-lane halves
+// (l and l ^ 32) in the VALU, where a 64-lane shuffle would take a round
+// trip through the LDS crossbar; each returns {this row's value, the
+// partner's} in an order that is the same pair on both lanes, and max and
+// fp32 addition are commutative, so the results equal the shuffles' bits.
+__device__ __forceinline__ float2 swap_rows16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, v),
+                                                  __builtin_bit_cast(uint32_t, v), false, false);
+  return float2{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
+__device__ __forceinline__ float2 swap_halves32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                  __builtin_bit_cast(uint32_t, v), false, false);
+  return float2{__builtin_bit_cast(float, (uint32_t)r[0]), __builtin_bit_cast(float, (uint32_t)r[1])};
+}
 __device__ __forceinline__ float max_over_groups16(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+  float2 p = swap_rows16(v);
+  v = fmaxf(p.x, p.y);
+  p = swap_halves32(v);
+  return fmaxf(p.x, p.y);
 }
 __device__ __forceinline__ float sum_over_groups16(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+  float2 p = swap_rows16(v);
+  v = p.x + p.y;
+  p = swap_halves32(v);
+  return p.x + p.y;
 }
 
 // Exclusive prefix sum of v over the THREADS threads of the workgroup (every

@@ -491,7 +491,10 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
             for (int i = 0; i < 16; ++i) mxs = fmaxf(mxs, s[rb][mt][i]);
           mxs *= p.scale_log2;  // > 0: max commutes with it
         }
-        mxs = fmaxf(mxs, __shfl_xor(mxs, 32));
+        {
+          const float2 hv = swap_halves32(mxs);  // the row's two halves of the tile
+          mxs = fmaxf(hv.x, hv.y);
+        }
         if (__builtin_amdgcn_ballot_w64(mxs > m[rb] + kRescaleSlack)) {
           const float m_new = fmaxf(m[rb], mxs);
           const float alpha =
@@ -575,7 +578,8 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
     // ---- epilogue: O^T / l, lane's row, 4 consecutive d per register quad
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb) {
-      const float l_tot = l[rb] + __shfl_xor(l[rb], 32);
+      const float2 lh = swap_halves32(l[rb]);
+      const float l_tot = lh.x + lh.y;
       if (!rvalid[rb]) continue;
       const int row = 32 * (RB * wave + rb) + col;
       const int qi = q_lo + row / g;
