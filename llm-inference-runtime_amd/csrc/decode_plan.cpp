@@ -257,16 +257,29 @@ static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_in
   // one.  On the 70B-shaped e4m3 batch it takes the step's fetched bytes
   // from 1.032 to 1.003 times the algorithmic bytes, at the same speed; on
   // the 4-head TinyLlama batch (no scales) it measured 0.1 us slower.
+  // (An affine partition at the round bound 4 ceil(mean / 4) cannot be
+  // beaten, so the unconstrained one is then not built.)
   Part part;
   const bool can_affine = shared_xcd_affine() && n_wg % kXcds == 0 && n_wg >= kXcds && hkv >= 8;
-  const int64_t top_free = partition(false, &part);
+  bool have = false;
+  int64_t top_aff = 0;
   if (can_affine) {
-    Part aff;
-    const int64_t top_aff = partition(true, &aff);
+    top_aff = partition(true, &part);
     bool fits = true;
-    for (const auto& list : aff.per) fits = fits && (int)list.size() <= kSharedMaxItems;
-    if (fits && (top_aff + 3) / 4 <= (top_free + 3) / 4) part = std::move(aff);
+    for (const auto& list : part.per) fits = fits && (int)list.size() <= kSharedMaxItems;
+    int64_t sum = 0;
+    for (int64_t l : part.load) sum += l;
+    const int64_t bound = 4 * (((sum + n_wg - 1) / n_wg + 3) / 4);
+    have = fits && top_aff <= bound;
+    if (fits && !have) {
+      Part free_part;
+      const int64_t top_free = partition(false, &free_part);
+      have = (top_aff + 3) / 4 <= (top_free + 3) / 4;
+      if (!have) part = std::move(free_part);
+      have = true;
+    }
   }
+  if (!have) partition(false, &part);
   std::vector<std::vector<int32_t>>& per = part.per;
   std::vector<int64_t>& load = part.load;
   // the kernel walks a workgroup's items in list order: longest first
