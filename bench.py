@@ -41,6 +41,8 @@ BF16_PEAK_TFLOPS = 2500.0
 WS_BYTES = 128 << 20
 CONFIGS = ("c2", "c3", "c4", "c4b", "c5d", "c5p", "devplan", "kvwrite")
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+# device time the prefill launches run untimed before they are timed
+PREFILL_SETTLE_MS = 150.0
 CSRC = os.path.join(ROOT, "llm-inference-runtime_amd", "csrc")
 
 
@@ -85,17 +87,43 @@ def _fill_queue(ms: float = 3.0) -> None:
         pagedattn.copy_bytes(_busy[1], _busy[0])
 
 
-def time_steps(fn, steps: int, warmup: int) -> list[float]:
+def settle(fn, min_ms: float, max_calls: int = 2000) -> int:
+    """Untimed calls of fn until min_ms of device time have passed (at most
+    max_calls); returns the number of calls.  The MFMA-bound prefill needs
+    this: its launch time falls by about 10 % over the first ~100 ms of
+    back-to-back launches and then holds (Llama-3-8B prefill on MI355X:
+    228 -> 205 us), while the HBM-bound decode steps are flat from the
+    first call."""
+    import torch
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    n, chunk, spent = 0, 8, 0.0
+    while spent < min_ms and n < max_calls:
+        a.record()
+        for i in range(chunk):
+            fn(n + i)
+        b.record()
+        b.synchronize()
+        spent += a.elapsed_time(b)
+        n += chunk
+    return n
+
+
+def time_steps(fn, steps: int, warmup: int, fill: bool = True) -> list[float]:
     """Per-step device time (ms): a HIP event pair around every call, on the
-    stream the library launches on (torch's current stream), with the steps
-    queued behind a few ms of other work (_fill_queue)."""
+    stream the library launches on (torch's current stream).  With `fill`
+    the steps are queued behind a few ms of other work (_fill_queue), so
+    that short steps run back to back; launches of hundreds of us keep the
+    queue ahead by themselves and are timed without it (the fill's copy
+    kernels slow the MFMA-bound launches after them by 2-3 %)."""
     import torch
     for i in range(warmup):
         fn(i)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(steps)]
     torch.cuda.synchronize()
-    _fill_queue(0.15 * steps + 1.0)
+    if fill:
+        _fill_queue(0.15 * steps + 1.0)
     for i, (a, b) in enumerate(evs):
         a.record()
         fn(warmup + i)
@@ -109,10 +137,12 @@ def _stats(ms: list[float]) -> dict:
             "ms_min": min(ms), "ms_max": max(ms), "iterations": len(ms)}
 
 
-def _time_graph_ms(fn, steps: int, warmup: int) -> float:
+def _time_graph_ms(fn, steps: int, warmup: int, settle_ms: float = 0.0) -> float:
     """Device time per call of fn: `steps` calls captured in one HIP graph,
     replayed and timed, so the host's per-call argument checks (tens of us
-    for a small launch) stay out of the figure."""
+    for a small launch) stay out of the figure.  With settle_ms the graph is
+    first replayed untimed for that much device time and the median of three
+    timed replays is taken (see settle)."""
     import torch
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -127,13 +157,18 @@ def _time_graph_ms(fn, steps: int, warmup: int) -> float:
             fn(i)
     g.replay()
     torch.cuda.synchronize()
-    start = torch.cuda.Event(enable_timing=True)
-    end = torch.cuda.Event(enable_timing=True)
-    start.record()
-    g.replay()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) / steps
+    if settle_ms > 0:
+        settle(lambda i: g.replay(), settle_ms)
+    times = []
+    for _ in range(3 if settle_ms > 0 else 1):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        g.replay()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / steps)
+    return statistics.median(times)
 
 
 def cpu_model() -> str:
@@ -330,8 +365,10 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         t = inst[i % reps]
         pw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps])
 
-    st_step = _stats(time_steps(step, args.steps, args.warmup))
-    st = _stats(time_steps(attn, args.steps, args.warmup))
+    # steady state: launch times settle after ~100 ms of back-to-back launches
+    settle_calls = settle(attn, PREFILL_SETTLE_MS)
+    st_step = _stats(time_steps(step, args.steps, args.warmup, fill=False))
+    st = _stats(time_steps(attn, args.steps, args.warmup, fill=False))
     ms = st["ms_median"]
     # the same attention with the q-tile list cut on the device by every run
     # (pagedattn_prefill_plan_device: a one-workgroup plan launch ahead of
@@ -345,8 +382,8 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         t = inst[i % reps]
         pd.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps])
 
-    dev_ms = _stats(time_steps(attn_dev, args.steps, args.warmup))["ms_median"]
-    dev_graph_ms = _time_graph_ms(attn_dev, args.steps, args.warmup)
+    dev_ms = _stats(time_steps(attn_dev, args.steps, args.warmup, fill=False))["ms_median"]
+    dev_graph_ms = _time_graph_ms(attn_dev, args.steps, args.warmup, settle_ms=PREFILL_SETTLE_MS)
     # a captured engine step: the list cut once for the step (update_plan,
     # as plan_prefill once per step) and every layer's run reading it
     layers = 32  # Llama-3-8B decoder layers
@@ -356,7 +393,7 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         for layer in range(layers):
             attn_dev(i * layers + layer)
 
-    step_graph_ms = _time_graph_ms(engine_step, 2, 1) / layers
+    step_graph_ms = _time_graph_ms(engine_step, 2, 1, settle_ms=PREFILL_SETTLE_MS) / layers
     dropped = int(ws_dev[12:16].view(torch.int32).item())
     res = {
         "workload": label,
@@ -367,6 +404,9 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         "rows": int(w.meta.nnz),
         "kv_tokens": int(w.meta.seq_lens.sum()),
         "replicas": reps,
+        "timing": f"after {settle_calls} untimed launches ({PREFILL_SETTLE_MS:.0f} ms of device "
+                  "time, where launch times have settled), then per-launch HIP events without a "
+                  "queue fill",
         "device_plan": {"attn_ms_median": round(dev_ms, 5),
                         "attn_TFLOPs": flops / (dev_ms * 1e-3) / 1e12,
                         "graph_ms_per_run": round(dev_graph_ms, 5),
