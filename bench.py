@@ -43,6 +43,10 @@ CONFIGS = ("c2", "c3", "c4", "c4b", "c5d", "c5p", "devplan", "kvwrite")
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 # device time the prefill launches run untimed before they are timed
 PREFILL_SETTLE_MS = 150.0
+DECODE_TIMING = ("K back-to-back steps between one HIP event pair on the launch stream "
+                 "(queued behind a few ms of copies), divided by K")
+PREFILL_TIMING = ("K back-to-back launches between one HIP event pair on the launch stream "
+                  "(queued behind two untimed launches), divided by K")
 CSRC = os.path.join(ROOT, "llm-inference-runtime_amd", "csrc")
 
 
@@ -132,6 +136,34 @@ def time_steps(fn, steps: int, warmup: int, fill: bool = True) -> list[float]:
     return [a.elapsed_time(b) for a, b in evs]
 
 
+def time_block(fn, steps: int, warmup: int, fill: bool = True) -> float:
+    """Device time per call (ms) of `steps` back-to-back calls of fn between
+    one HIP event pair, after `warmup` untimed calls: the whole-job rate of
+    a stream of steps.  The calls are queued behind other work so that the
+    GPU never waits for the host between the events: a few ms of copies
+    (_fill_queue), or with fill=False two untimed calls of fn itself (for
+    launches of hundreds of us, which keep ahead of the host on their own
+    and which the copy kernels slow by 2-3 %)."""
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    if fill:
+        _fill_queue(0.15 * steps + 1.0)
+    else:
+        fn(warmup)
+        fn(warmup + 1)
+        warmup += 2
+    a.record()
+    for i in range(steps):
+        fn(warmup + i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
 def _stats(ms: list[float]) -> dict:
     return {"ms_median": statistics.median(ms), "ms_mean": statistics.fmean(ms),
             "ms_min": min(ms), "ms_max": max(ms), "iterations": len(ms)}
@@ -213,13 +245,14 @@ def load_traffic(workload: str) -> dict:
 
 
 def roofline(bound: str, kernel: str, achieved: float, work: int, ms: float,
-             workload: str) -> dict:
+             workload: str, timing: str) -> dict:
     peak = HBM_PEAK_GBS if bound == "hbm" else BF16_PEAK_TFLOPS
     r = {"bound": bound, "kernel": kernel, "achieved": round(achieved, 2), "peak": peak,
          "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(achieved / peak, 4)}
     r.update(load_traffic(workload))
     r["alg_bytes_per_launch" if bound == "hbm" else "alg_flops_per_launch"] = work
-    r["launch_ms_median"] = round(ms, 5)
+    r["launch_ms"] = round(ms, 5)
+    r["launch_timing"] = timing
     return r
 
 
@@ -269,11 +302,15 @@ def bench_decode(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         dw.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps], append_key=t.k_new,
                append_value=t.v_new)
 
-    st = _stats(time_steps(step, args.steps, args.warmup))
-    ms = st["ms_median"]
+    # the steps as a stream (the rate reported), then each step between
+    # its own event pair (spread statistics; each pair adds ~2-3 us)
+    ms = time_block(step, args.steps, args.warmup)
+    st = _stats(time_steps(step, args.steps, 1))
     res = {
         "workload": label,
-        **{k: round(v, 5) if isinstance(v, float) else v for k, v in st.items()},
+        "ms_per_step": round(ms, 5),
+        "per_step_events_ms": {k: round(v, 5) if isinstance(v, float) else v
+                               for k, v in st.items()},
         "step_GBps": alg_step / (ms * 1e-3) / 1e9,
         "alg_bytes_step": alg_step,
         "alg_bytes_attn": alg_attn,
@@ -285,7 +322,8 @@ def bench_decode(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         "plan_kind": kind,
     }
     res["frac"] = res["step_GBps"] / HBM_PEAK_GBS
-    res["roofline"] = roofline("hbm", kernel, res["step_GBps"], alg_step, ms, label)
+    res["roofline"] = roofline("hbm", kernel, res["step_GBps"], alg_step, ms, label,
+                               DECODE_TIMING)
     if cpu_seqs is not None:
         res["cpu_baseline"] = cpu_decode_baseline(w, inst[0], cpu_seqs, kv_elem)
     del inst, outs
@@ -367,9 +405,11 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
 
     # steady state: launch times settle after ~100 ms of back-to-back launches
     settle_calls = settle(attn, PREFILL_SETTLE_MS)
-    st_step = _stats(time_steps(step, args.steps, args.warmup, fill=False))
-    st = _stats(time_steps(attn, args.steps, args.warmup, fill=False))
-    ms = st["ms_median"]
+    # the launches as a stream (the rate reported), then each launch between
+    # its own event pair (spread statistics)
+    ms = time_block(attn, args.steps, args.warmup, fill=False)
+    step_ms = time_block(step, args.steps, args.warmup, fill=False)
+    st = _stats(time_steps(attn, args.steps, 1, fill=False))
     # the same attention with the q-tile list cut on the device by every run
     # (pagedattn_prefill_plan_device: a one-workgroup plan launch ahead of
     # the attention), eagerly and `steps` runs replayed from one HIP graph
@@ -382,7 +422,7 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         t = inst[i % reps]
         pd.run(t.q, t.pool, kv_scales=t.scales, out=outs[i % reps])
 
-    dev_ms = _stats(time_steps(attn_dev, args.steps, args.warmup, fill=False))["ms_median"]
+    dev_ms = time_block(attn_dev, args.steps, args.warmup, fill=False)
     dev_graph_ms = _time_graph_ms(attn_dev, args.steps, args.warmup, settle_ms=PREFILL_SETTLE_MS)
     # a captured engine step: the list cut once for the step (update_plan,
     # as plan_prefill once per step) and every layer's run reading it
@@ -397,17 +437,18 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
     dropped = int(ws_dev[12:16].view(torch.int32).item())
     res = {
         "workload": label,
-        **{k: round(v, 5) if isinstance(v, float) else v for k, v in st.items()},
-        "step_ms_median": round(st_step["ms_median"], 5),
+        "ms_per_launch": round(ms, 5),
+        "per_launch_events_ms": {k: round(v, 5) if isinstance(v, float) else v
+                                 for k, v in st.items()},
+        "step_ms_per_step": round(step_ms, 5),
         "attn_TFLOPs": flops / (ms * 1e-3) / 1e12,
         "alg_flops_attn": flops,
         "rows": int(w.meta.nnz),
         "kv_tokens": int(w.meta.seq_lens.sum()),
         "replicas": reps,
         "timing": f"after {settle_calls} untimed launches ({PREFILL_SETTLE_MS:.0f} ms of device "
-                  "time, where launch times have settled), then per-launch HIP events without a "
-                  "queue fill",
-        "device_plan": {"attn_ms_median": round(dev_ms, 5),
+                  f"time, where launch times have settled): {PREFILL_TIMING}",
+        "device_plan": {"attn_ms_per_launch": round(dev_ms, 5),
                         "attn_TFLOPs": flops / (dev_ms * 1e-3) / 1e12,
                         "graph_ms_per_run": round(dev_graph_ms, 5),
                         "graph_TFLOPs": flops / (dev_graph_ms * 1e-3) / 1e12,
@@ -421,7 +462,8 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
                                 "runs reading its list, per run"},
     }
     res["frac"] = res["attn_TFLOPs"] / BF16_PEAK_TFLOPS
-    res["roofline"] = roofline("mfma", kernel, res["attn_TFLOPs"], flops, ms, label)
+    res["roofline"] = roofline("mfma", kernel, res["attn_TFLOPs"], flops, ms, label,
+                               PREFILL_TIMING)
     if cpu_seqs is not None:
         res["cpu_baseline"] = cpu_prefill_baseline(w, inst[0], cpu_seqs)
     del inst, outs, ws_dev
@@ -714,16 +756,18 @@ def main() -> int:
         r = bench_decode(main_w, args, dev, dtype, "tinyllama_decode",
                          list(range(main_w.meta.batch_size)) if cpu else None,
                          {"split": DECODE_KERNEL["c2"], "shared": DECODE_KERNEL["c2.shared"]})
-        log(f"tinyllama_decode: step {r['ms_median'] * 1e3:.1f} us (median) = "
-            f"{r['step_GBps']:.0f} GB/s ({100 * r['frac']:.1f}% of 8 TB/s)")
+        log(f"tinyllama_decode: step {r['ms_per_step'] * 1e3:.1f} us = "
+            f"{r['step_GBps']:.0f} GB/s ({100 * r['frac']:.1f}% of 8 TB/s); "
+            f"{r['per_step_events_ms']['ms_median'] * 1e3:.1f} us median with an event "
+            f"pair per step")
     sub = argparse.Namespace(steps=steps_n, warmup=3)
     if "c3" in want:
         pw = W.llama3_8b_prefill(seed=args.seed)
         pr = bench_prefill(pw, sub, dev, dtype, "llama3_8b_prefill",
                            list(range(pw.meta.batch_size)) if cpu else None, PREFILL_KERNEL["c3"])
-        log(f"llama3_8b_prefill: {pr['ms_median'] * 1e3:.1f} us = {pr['attn_TFLOPs']:.1f} "
+        log(f"llama3_8b_prefill: {pr['ms_per_launch'] * 1e3:.1f} us = {pr['attn_TFLOPs']:.1f} "
             f"TFLOP/s ({100 * pr['frac']:.1f}% of bf16 peak); device plan "
-            f"{pr['device_plan']['attn_ms_median'] * 1e3:.1f} us eager, "
+            f"{pr['device_plan']['attn_ms_per_launch'] * 1e3:.1f} us eager, "
             f"{pr['device_plan']['graph_ms_per_run'] * 1e3:.1f} us from a graph")
         extra["llama3_8b_prefill"] = pr
     if "c4" in want or "c4b" in want:
@@ -731,7 +775,7 @@ def main() -> int:
         if "c4" in want:
             lr = bench_decode(lw, sub, dev, dtype, "llama3_8b_long_decode",
                               [0] if cpu else None, DECODE_KERNEL["c4"])
-            log(f"llama3_8b_long_decode: {lr['ms_median'] * 1e3:.0f} us = {lr['step_GBps']:.0f} "
+            log(f"llama3_8b_long_decode: {lr['ms_per_step'] * 1e3:.0f} us = {lr['step_GBps']:.0f} "
                 f"GB/s ({100 * lr['frac']:.1f}%)")
             extra["llama3_8b_long_decode"] = lr
         if "c4b" in want:
@@ -784,7 +828,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(r["ms_median"], 5),
+        "ms_per_step": round(r["ms_per_step"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -798,12 +842,11 @@ def main() -> int:
             "page_size": 16,
             "parallelism": "single GPU",
             "seed": args.seed,
-            "timing": "per-step HIP events on the launch stream; ms_per_step is the median",
+            "timing": DECODE_TIMING + "; step_stats_ms: an event pair around each step",
         },
         "roofline": r["roofline"],
         "cpu_baseline": r.get("cpu_baseline"),
-        "step_stats_ms": {k: r[k] for k in ("ms_median", "ms_mean", "ms_min", "ms_max",
-                                            "iterations")},
+        "step_stats_ms": r["per_step_events_ms"],
         "extra": extra,
         "calibration": cal,
     }
