@@ -124,12 +124,19 @@ static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_in
     const int32_t np = npages[id / hkv];
     return std::max<int32_t>(1, ((np + 1) / 2 + chunk_pages / 2 - 1) / (chunk_pages / 2));
   };
-  std::vector<int32_t> order((size_t)n_all);
-  for (int64_t i = 0; i < n_all; ++i) order[(size_t)i] = (int32_t)i;
-  // sequence-major item ids; longest first, ties in id order
-  std::stable_sort(order.begin(), order.end(), [&](int32_t a, int32_t c) {
-    return npages[a / hkv] > npages[c / hkv];
-  });
+  std::vector<int32_t> ck((size_t)n_all);  // chunks of each item
+  for (int64_t i = 0; i < n_all; ++i) ck[(size_t)i] = chunks_of((int32_t)i);
+  // sequence-major item ids b hkv + h; longest first, ties in id order.  The
+  // heads of a sequence share its key, so the sequences are sorted and each
+  // expanded into its heads in order.
+  std::vector<int32_t> seqs((size_t)batch);
+  for (int b = 0; b < batch; ++b) seqs[(size_t)b] = b;
+  std::stable_sort(seqs.begin(), seqs.end(),
+                   [&](int32_t a, int32_t c) { return npages[a] > npages[c]; });
+  std::vector<int32_t> order;
+  order.reserve((size_t)n_all);
+  for (int32_t b : seqs)
+    for (int h = 0; h < hkv; ++h) order.push_back(b * hkv + h);
   const int n_wg = (int)std::min<int64_t>(std::max(cus, 1), n_all);
   // One partition: longest first (per XCD with `affine`), then the
   // refinement below.  Returns the chunks of its busiest workgroup.
@@ -139,6 +146,7 @@ static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_in
   };
   auto partition = [&](bool affine, Part* out) -> int64_t {
     std::vector<std::vector<int32_t>> per(n_wg);
+    for (auto& list : per) list.reserve(kSharedMaxItems + 1);
     std::vector<int64_t> load(n_wg, 0);
     int64_t total = 0;
     // longest first onto the least-loaded workgroup among `wgs`
@@ -150,8 +158,8 @@ static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_in
         auto top = heap.top();
         heap.pop();
         per[top.second].push_back(id);
-        top.first += chunks_of(id);
-        total += chunks_of(id);
+        top.first += ck[id];
+        total += ck[id];
         load[top.second] = top.first;
         heap.push(top);
       }
@@ -172,7 +180,7 @@ static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_in
         for (int y = 1; y < kXcds; ++y)
           if (xcd_load[y] < xcd_load[x]) x = y;
         for (int h = 0; h < hkv; ++h) xcd_ids[x].push_back(b * hkv + h);
-        xcd_load[x] += (int64_t)hkv * chunks_of(b * hkv);
+        xcd_load[x] += (int64_t)hkv * ck[(size_t)b * hkv];
       }
       for (int x = 0; x < kXcds; ++x) {
         std::vector<int> wgs;
@@ -202,7 +210,7 @@ static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_in
       by_load.insert(std::lower_bound(by_load.begin(), by_load.end(), x, lighter), x);
     };
     auto by_size = [&](int32_t x, int32_t y) {
-      return chunks_of(x) > chunks_of(y) || (chunks_of(x) == chunks_of(y) && x < y);
+      return ck[x] > ck[y] || (ck[x] == ck[y] && x < y);
     };
     for (int iter = 0; iter < n_wg; ++iter) {
       const int w = by_load.back();
@@ -210,9 +218,11 @@ static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_in
       if (top <= round_bound) break;
       bool done = false;
       int partner = -1;
-      // the busiest workgroup's items, largest first (lists are kept in that order)
+      // the busiest workgroup's items, largest first (every list is kept in
+      // non-increasing chunk order: longest first from the LPT pass, by_size
+      // after each step)
       for (size_t i = 0; i < per[w].size() && !done; ++i) {
-        const int64_t a = chunks_of(per[w][i]);
+        const int64_t a = ck[per[w][i]];
         for (int v : by_load) {
           if (v == w) continue;
           if (load[v] + 1 >= top) break;
@@ -225,18 +235,20 @@ static bool plan_shared(const std::vector<int32_t>& npages, const int32_t* kv_in
             done = true;
             break;
           }
-          for (size_t j = 0; j < per[v].size(); ++j) {
-            const int64_t b = chunks_of(per[v][j]);
-            if (b < a && load[w] - a + b < top && load[v] - b + a < top) {
-              std::swap(per[w][i], per[v][j]);
-              load[w] += b - a;
-              load[v] += a - b;
-              partner = v;
-              done = true;
-              break;
-            }
+          // a swap for a smaller item b of v needs a - b < top - load[v] (the
+          // busiest side then drops by a - b > 0): the first item of v below a
+          // is the largest such b, so if it does not fit, none does
+          size_t j = 0;
+          while (j < per[v].size() && ck[per[v][j]] >= a) ++j;
+          if (j < per[v].size() && load[v] - ck[per[v][j]] + a < top) {
+            const int64_t b = ck[per[v][j]];
+            std::swap(per[w][i], per[v][j]);
+            load[w] += b - a;
+            load[v] += a - b;
+            partner = v;
+            done = true;
+            break;
           }
-          if (done) break;
         }
       }
       if (!done) break;
