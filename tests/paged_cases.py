@@ -4,8 +4,10 @@ lengths, run helpers for the HIP path, and the oracle comparisons."""
 from __future__ import annotations
 
 import math
+import os
 
 import numpy as np
+import pytest
 import torch
 
 import oracle as O
@@ -13,6 +15,21 @@ import pagedattn
 from pagedattn.metadata import decode_metadata, prefill_metadata
 
 WS_BYTES = 128 * 1024 * 1024
+
+
+def require_shared_plans():
+    """Skip a test of the shared-item decode plans when the environment
+    switches them off (the planner knob PAGEDATTN_DECODE_SHARED=0)."""
+    if os.environ.get("PAGEDATTN_DECODE_SHARED") == "0":
+        pytest.skip("PAGEDATTN_DECODE_SHARED=0 switches shared-item decode plans off")
+
+
+def require_fixed_chunks():
+    """Skip a bit-equality test of shared-item decode when the environment
+    selects arrival-order chunk claims (PAGEDATTN_DECODE_DETERMINISTIC=0),
+    under which repeated runs may differ in the last bits."""
+    if os.environ.get("PAGEDATTN_DECODE_DETERMINISTIC") == "0":
+        pytest.skip("PAGEDATTN_DECODE_DETERMINISTIC=0 claims chunks in arrival order")
 
 
 def workspace(device) -> torch.Tensor:

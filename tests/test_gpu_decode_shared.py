@@ -18,7 +18,8 @@ import pagedattn
 from pagedattn import workloads as W
 
 from paged_cases import (decode_case, i32, log2_max_jumps, lse_err, max_err, oracle_decode,
-                         rel_err, scale_keys_by_page, workspace)
+                         rel_err, require_fixed_chunks, require_shared_plans,
+                         scale_keys_by_page, workspace)
 
 pytestmark = pytest.mark.gpu
 
@@ -106,6 +107,7 @@ def test_shared_eight_items_per_workgroup(gpu, shared):
 
 
 def test_shared_ragged_batch(gpu, shared):
+    require_fixed_chunks()
     # several items of different lengths per workgroup, including items of a
     # single chunk next to items that all four waves share; the default
     # assignment is fixed, so repeated runs are bit-identical
@@ -289,6 +291,7 @@ def test_shared_rescale_branch(gpu, shared, fp8):
 
 
 def test_shared_is_the_default_for_tinyllama(gpu, monkeypatch):
+    require_shared_plans()
     # the TinyLlama B=256 batch balances over the CUs as whole items, so the
     # default plan is the shared one; it agrees with the split plan and the
     # oracle (which the at-scale decode tests also check)

@@ -19,7 +19,7 @@ import pagedattn
 from pagedattn.metadata import decode_metadata, prefill_metadata
 
 from paged_cases import (decode_case, i32, lse_err, max_err, oracle_decode, random_tables,
-                         run_decode, workspace)
+                         require_fixed_chunks, require_shared_plans, run_decode, workspace)
 
 pytestmark = pytest.mark.gpu
 
@@ -264,6 +264,9 @@ def test_decode_step_graph_replay(gpu, bsz, hq, hkv, d, kind, table):
     """The graphed step (with `table`: metadata, update_plan and the run
     captured together) equals the eager step that deals in every run, bit
     for bit, every replay."""
+    if kind == "device_shared":
+        require_shared_plans()
+        require_fixed_chunks()
     rng = np.random.default_rng(11)
     start = [int(x) for x in rng.integers(1, 3000, bsz)]
     start[0], start[1] = 15, 16  # crosses a page boundary in the first replays
@@ -332,6 +335,8 @@ def test_decode_step_graph_replay(gpu, bsz, hq, hkv, d, kind, table):
 def test_device_shared_plan(gpu, name, lens, hq, hkv, d, fp8):
     """The device-dealt shared-item partition: one launch, repeated runs
     bit-identical, outputs and lse against the oracle, faults counter zero."""
+    require_shared_plans()
+    require_fixed_chunks()
     lens = [int(x) for x in lens]
     meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=len(lens) + 3)
     scales = None
@@ -371,6 +376,8 @@ def test_device_shared_table_equals_dealing(gpu, name, lens, hq, hkv, d, fp8):
     """update_plan deals the items once into the workspace; the runs that
     read that table give the bits of runs that deal in their prologue, and
     the table follows the metadata of each update."""
+    require_shared_plans()
+    require_fixed_chunks()
     lens = [int(x) for x in lens]
     meta, pool, q = decode_case(gpu, lens, hq, hkv, d, seed=len(lens) + 5)
     scales = None
