@@ -388,8 +388,12 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
     ws = torch.zeros(WS_BYTES, dtype=torch.uint8, device=dev)
     pw = pagedattn.BatchPrefillWithPagedKVCacheWrapper(ws, "HND")
     t0 = inst[0]
+    torch.cuda.synchronize()
+    tp = time.perf_counter()
     pw.plan(t0.qo_indptr, t0.kv_indptr, t0.kv_indices, t0.kv_last_page_len, w.hq, w.hkv, w.d,
             16, q_data_type=dtype, causal=True)
+    torch.cuda.synchronize()
+    plan_ms = (time.perf_counter() - tp) * 1e3
     outs = [torch.empty_like(t.q) for t in inst]
 
     def step(i):
@@ -445,6 +449,7 @@ def bench_prefill(w, args, dev, dtype, label: str, cpu_seqs: list[int] | None,
         "alg_flops_attn": flops,
         "rows": int(w.meta.nnz),
         "kv_tokens": int(w.meta.seq_lens.sum()),
+        "plan_ms_host": plan_ms,
         "replicas": reps,
         "timing": f"after {settle_calls} untimed launches ({PREFILL_SETTLE_MS:.0f} ms of device "
                   f"time, where launch times have settled): {PREFILL_TIMING}",
