@@ -358,6 +358,9 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
       }
     }
 
+    // whether any row of this wave lies in the tile
+    const bool wave_rows = 32 * RB * wave < (q_hi - q_lo) * g;
+
     f32x16 o[RB][C::DT];
     float m[RB], l[RB];
 #pragma unroll
@@ -402,38 +405,10 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
     }
     int pid_next = fetch_page_ids(p, ind_lo, npages, 1, lane);
 
-    // Iteration t: (e4m3: convert and store tile t) -- barrier -- issue tile
-    // t + 1's loads into the other stage, interleaved with tile t's MFMAs.
-    // The loads are issued on every tile (on the last one with no page, so
-    // they read nothing) and tiles that need no mask run a copy of the step
-    // without it: the step is then one branch-free block apart from the
-    // rare rescale, and the compiler can overlap its LDS reads, exps and
-    // MFMAs across the phases.
-    auto step = [&](auto mask_tag, int t, uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+    // Tile t's QK, softmax and PV from stage `cur` (e4m3: with the register
+    // loads of tile t + 1, pages pid_ld, issued between its phases).
+    auto compute = [&](auto mask_tag, int t, uint8_t* cur, int pid_ld) __attribute__((always_inline)) {
       constexpr bool MASK = decltype(mask_tag)::value;
-      if constexpr (FP8) {
-        store_half<D, BF16, FP8, RB>(kr, cur, wave, lane);
-        store_half<D, BF16, FP8, RB>(vr, cur + C::TILEB, wave, lane);
-        ksc_l = kr.sc;
-        vsc_l = vr.sc;
-      }
-      // Every wave's direct-to-LDS loads of tile t are complete before any wave
-      // passes the barrier and reads them.  The barrier itself waits only for
-      // LDS operations (workgroup-scope release), so this wait is explicit
-      // rather than left to the compiler's alias tracking of the loads.
-      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-      __syncthreads();
-      pid = pid_next;
-      pid_next = fetch_page_ids(p, ind_lo, npages, t + 2, lane);
-      const int pid_ld = t + 1 < n_tiles ? pid : -1;  // past the last tile: no pages
-      if constexpr (!FP8) {
-        // tile t + 1 straight into the other stage, K and V, a whole tile
-        // ahead of the barrier that waits for it
-        dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid_ld, npages, last, t + 1, nxt, wave, lane);
-        dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid_ld, npages, last, t + 1, nxt + C::TILEB,
-                                             wave, lane);
-      }
-
       // ---- S^T = K . Q^T
       f32x16 s[RB][2];
 #pragma unroll
@@ -550,6 +525,41 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
         }
       }
     };
+    // Iteration t: (e4m3: convert and store tile t) -- barrier -- issue tile
+    // t + 1's loads into the other stage, interleaved with tile t's MFMAs.
+    // The loads are issued on every tile (on the last one with no page, so
+    // they read nothing) and tiles that need no mask run a copy of the step
+    // without it: the step is then one branch-free block apart from the
+    // rare rescale, and the compiler can overlap its LDS reads, exps and
+    // MFMAs across the phases.
+    auto step = [&](auto mask_tag, int t, uint8_t* cur, uint8_t* nxt) __attribute__((always_inline)) {
+      if constexpr (FP8) {
+        store_half<D, BF16, FP8, RB>(kr, cur, wave, lane);
+        store_half<D, BF16, FP8, RB>(vr, cur + C::TILEB, wave, lane);
+        ksc_l = kr.sc;
+        vsc_l = vr.sc;
+      }
+      // Every wave's direct-to-LDS loads of tile t are complete before any wave
+      // passes the barrier and reads them.  The barrier itself waits only for
+      // LDS operations (workgroup-scope release), so this wait is explicit
+      // rather than left to the compiler's alias tracking of the loads.
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      __syncthreads();
+      pid = pid_next;
+      pid_next = fetch_page_ids(p, ind_lo, npages, t + 2, lane);
+      const int pid_ld = t + 1 < n_tiles ? pid : -1;  // past the last tile: no pages
+      if constexpr (!FP8) {
+        // tile t + 1 straight into the other stage, K and V, a whole tile
+        // ahead of the barrier that waits for it
+        dma_half<D, BF16, FP8, RB, false, NW>(p, h, pid_ld, npages, last, t + 1, nxt, wave, lane);
+        dma_half<D, BF16, FP8, RB, true, NW>(p, h, pid_ld, npages, last, t + 1, nxt + C::TILEB,
+                                             wave, lane);
+      }
+      // paired tiles: a wave with no row of the tile only loads
+      if (!decltype(pair_tag)::value || wave_rows) compute(mask_tag, t, cur, pid_ld);
+    };
+
+
     // tiles [0, n_clean) lie wholly at or below the first row's diagonal
     // (and inside the sequence): no mask; the rest are masked.  Tile t uses
     // stage t & 1 (the prologue loaded tile 0 into stage 0).
@@ -605,10 +615,14 @@ __global__ void __launch_bounds__(64 * kPrefillWaves, 1) prefill_kernel(PrefillP
   if constexpr (PAIRS) {
     if (paired) {
       const int h0 = h & ~1;
+      // The odd head's row blocks run in reverse wave order.  Waves w and
+      // w + WAVES/2 share a SIMD, so a pair of tiles with few rows puts its
+      // working waves on different SIMDs (waves without rows skip the
+      // compute).
       if (wave < C::WAVES / 2)
         body(std::true_type{}, stage0, stage1, wave, h0);
       else
-        body(std::true_type{}, stage2, stage3, wave - C::WAVES / 2, h0 + 1);
+        body(std::true_type{}, stage2, stage3, C::WAVES - 1 - wave, h0 + 1);
       return;
     }
   }
